@@ -1,0 +1,277 @@
+#!/usr/bin/env python3
+"""Benchmark of the XCD-domain kernels on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--all]
+
+A step is one pass of the hot path over one batch of synthetic input already resident in
+HBM: one GEMV call, one histogram of 2^28 keys, ... W untimed warm-up steps, then exactly K
+steps timed with HIP events on the stream the kernels are launched on. Prints ONE JSON line.
+`value` is the XCD-aware variant's throughput; the oblivious and rotated variants are
+timed over the same K steps and reported beside it with the aware/oblivious speedup.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "GEMV GB/s (% HBM peak); hist Gkeys/s; XCD-aware vs oblivious speedup"
+MODES = ("oblivious", "aware", "rotated")
+
+
+def _cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+# ---------------------------------------------------------------------------------------
+# Workloads
+# ---------------------------------------------------------------------------------------
+class GemvF32:
+    """configs[0]: fp32 y = A.x, A 4096x4096 and x from U[-1,1) (seed 4242)."""
+    name = "gemv_f32_4096x4096"
+    unit = "GB/s"
+    dtype = "f32"
+
+    def __init__(self, M=4096, K=4096):
+        import numpy as np
+        import torch
+        from l2domain_amd import gen
+        self.M, self.K = M, K
+        A, x = gen.gemv_f32_inputs(M, K)
+        self.hA, self.hx = A, x
+        self.A = torch.from_numpy(A).cuda()
+        self.x = torch.from_numpy(x).cuda()
+        self.y = torch.empty(M, dtype=torch.float32, device="cuda")
+        self.bytes = 4 * M * K + 4 * K + 4 * M
+        self.np = np
+
+    def step(self, mode):
+        from l2domain_amd.gemv import gemv
+        gemv(self.A, self.x, self.y, mode=mode)
+
+    def throughput(self, sec_per_step):
+        return self.bytes / sec_per_step / 1e9
+
+    def verify(self):
+        import oracle as ora
+        ref, yabs = ora.gemv_f64(self.hA, self.hx, nthreads=_cpu_threads())
+        ok = True
+        for mode in MODES:
+            self.step(mode)
+            y = self.y.cpu().numpy()
+            rel = float(self.np.max(self.np.abs(y - ref)) / self.np.max(self.np.abs(ref)))
+            ok = ok and rel <= 1e-3
+        return ok
+
+    def roofline(self, sec_per_launch):
+        achieved = self.bytes / sec_per_launch / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "gemv_kernel<false,16>", "algorithmic_bytes_per_launch": self.bytes}
+
+    def config(self):
+        return {"workload": self.name, "M": self.M, "K": self.K, "dtype": "fp32", "seed": 4242}
+
+    def cpu_baseline(self):
+        import oracle as ora
+        nt = _cpu_threads()
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 2.0:
+            ora.gemv_f32_seq(self.hA, self.hx, nthreads=nt)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(self.bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+                "sample": f"{reps} full 4096x4096 fp32 GEMVs (oracle fp32 row loop, GEMV.cu:383-390)"}
+
+
+class GemvF16(GemvF32):
+    """configs[2]: fp16 W (N(0,0.02), seed 4243), x (N(0,1), seed 4244), fp32 accumulate."""
+    dtype = "f16->f32"
+
+    def __init__(self, M=14336, K=4096):
+        import numpy as np
+        import torch
+        from l2domain_amd import gen
+        self.M, self.K = M, K
+        self.name = f"gemv_f16_{M}x{K}"
+        W, x = gen.gemv_f16_inputs(M, K)
+        self.hA, self.hx = W, x
+        self.A = torch.from_numpy(W).cuda()
+        self.x = torch.from_numpy(x).cuda()
+        self.y = torch.empty(M, dtype=torch.float32, device="cuda")
+        self.bytes = 2 * M * K + 2 * K + 4 * M
+        self.np = np
+
+    def verify(self):
+        import oracle as ora
+        ref, _ = ora.gemv_f64(self.hA, self.hx, nthreads=_cpu_threads())
+        ok = True
+        for mode in MODES:
+            self.step(mode)
+            y = self.y.cpu().numpy()
+            ok = ok and float(self.np.max(self.np.abs(y - ref)) / self.np.max(self.np.abs(ref))) <= 2e-2
+        return ok
+
+    def roofline(self, sec_per_launch):
+        r = super().roofline(sec_per_launch)
+        r["kernel"] = "gemv_kernel<true,*>"
+        return r
+
+    def config(self):
+        return {"workload": self.name, "M": self.M, "K": self.K, "dtype": "fp16 in, fp32 accumulate",
+                "seeds": [4243, 4244]}
+
+    def cpu_baseline(self):
+        import oracle as ora
+        nt = _cpu_threads()
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 2.0:
+            ora.gemv_f64(self.hA, self.hx, nthreads=nt)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(self.bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+                "sample": f"{reps} full {self.M}x{self.K} fp16 GEMVs (oracle row loop)"}
+
+
+WORKLOADS = {
+    "gemv_f32": GemvF32,
+    "gemv_f16_up": lambda: GemvF16(14336, 4096),
+    "gemv_f16_down": lambda: GemvF16(4096, 14336),
+}
+DEFAULT_WORKLOAD = "gemv_f32"
+
+
+# ---------------------------------------------------------------------------------------
+# Timing
+# ---------------------------------------------------------------------------------------
+def time_steps(wl, mode, steps, warmup, flusher=None):
+    """Returns seconds per step over exactly `steps` steps (HIP events on the launch stream)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        wl.step(mode)
+    torch.cuda.synchronize()
+    if flusher is None:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            wl.step(mode)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / steps
+    # cold: flush before each step, time each step separately
+    total = 0.0
+    for _ in range(steps):
+        flusher.flush()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        wl.step(mode)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        total += e0.elapsed_time(e1) / 1e3
+    return total / steps
+
+
+def run_workload(name, steps, warmup, cold=False, with_cpu=True):
+    import torch
+    from l2domain_amd.domain import CacheFlusher
+    wl = WORKLOADS[name]()
+    ok = wl.verify()
+    flusher = CacheFlusher() if cold else None
+    res = {}
+    for mode in MODES:
+        res[mode] = time_steps(wl, mode, steps, warmup, flusher)
+    torch.cuda.synchronize()
+    out = {
+        "workload": wl,
+        "verified": ok,
+        "sec": res,
+        "tput": {m: wl.throughput(s) for m, s in res.items()},
+    }
+    if with_cpu:
+        out["cpu"] = wl.cpu_baseline()
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    ap.add_argument("--cold", action="store_true", help="flush L2 + Infinity Cache before every step")
+    ap.add_argument("--all", action="store_true", help="also measure every other workload (extras)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py: this build measures one MI355X only (one-GPU tier); "
+              f"--gpus {args.gpus} / WORLD_SIZE={world} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm device visible", file=sys.stderr)
+        sys.exit(1)
+    from l2domain_amd.domain import topology
+
+    r = run_workload(args.workload, args.steps, args.warmup, cold=args.cold, with_cpu=not args.no_cpu)
+    wl = r["workload"]
+    sec = r["sec"]["aware"]
+    line = {
+        "metric": METRIC,
+        "value": round(r["tput"]["aware"], 3),
+        "unit": wl.unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl.dtype,
+        "data": "synthetic (seeded generators, inputs resident in HBM)",
+        "config": dict(wl.config(), cache="cold" if args.cold else "warm", mode="xcd_aware"),
+        "verified": r["verified"],
+        "modes": {m: {"ms_per_step": round(r["sec"][m] * 1e3, 6), "value": round(r["tput"][m], 3)}
+                  for m in MODES},
+        "speedup_aware_vs_oblivious": round(r["sec"]["oblivious"] / r["sec"]["aware"], 4),
+        "speedup_rotated_vs_oblivious": round(r["sec"]["oblivious"] / r["sec"]["rotated"], 4),
+        "roofline": wl.roofline(sec),
+        "cpu_baseline": r.get("cpu"),
+        "device": topology(0)["name"],
+    }
+    if args.all:
+        extras = {}
+        for name in sorted(WORKLOADS):
+            if name == args.workload:
+                continue
+            e = run_workload(name, args.steps, args.warmup, cold=args.cold, with_cpu=False)
+            extras[name] = {"verified": e["verified"], "unit": e["workload"].unit,
+                            "value_aware": round(e["tput"]["aware"], 3),
+                            "value_oblivious": round(e["tput"]["oblivious"], 3),
+                            "value_rotated": round(e["tput"]["rotated"], 3),
+                            "speedup_aware_vs_oblivious": round(e["sec"]["oblivious"] / e["sec"]["aware"], 4),
+                            "roofline": e["workload"].roofline(e["sec"]["aware"])}
+        line["extras"] = extras
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,130 @@
+/*
+ * xdom.h -- C ABI of libxdom, the MI355X (gfx950) XCD-domain kernel library.
+ *
+ * The reference (LyleLuo/L2Domain) has no library interface: its hot kernels are
+ * file-local `__global__` functions inside one executable per application, driven by
+ * positional argv and parsed from stdout. This header is the drop-in boundary that
+ * replaces those kernels; each entry point names the reference code it stands in for.
+ *
+ * Conventions (all entry points):
+ *   - Plain C types only. Device buffers are caller-owned device pointers; `stream` is a
+ *     hipStream_t passed as void* (NULL = the null stream).
+ *   - Return 0 (XD_OK) on success, a negative XD_ERR_* code on failure. Nothing aborts.
+ *     xd_last_error() gives a human-readable message for the calling thread.
+ *   - `mode` selects the work placement:
+ *       XD_MODE_OBLIVIOUS  default dispatch order, no XCD awareness (the reference's
+ *                          "baseline", e.g. gemv_baseline_kernel GEMV.cu:199-231);
+ *       XD_MODE_AWARE      every XCD owns one contiguous slice of the data (the reference's
+ *                          "aware", e.g. gemv_partitioned_kernel GEMV.cu:163-197);
+ *       XD_MODE_ROTATED    negative control: slice s is handled by XCD (s+r) mod 8, where the
+ *                          rotation r advances by one on every pass over the data (the
+ *                          reference's "swapped", GEMV.cu:176).
+ *   - Entry points that need scratch memory take a caller-owned workspace whose size is
+ *     given by the matching *_workspace_size() query (the reference's nullptr -> bytes
+ *     size-query idiom, utility/latopt.cuh:532-540). A workspace must be zeroed once
+ *     after allocation (hipMemset to 0); the kernels leave it zeroed again on exit.
+ *   - Work is stream-ordered; functions return after enqueueing unless stated otherwise.
+ */
+#ifndef XDOM_H
+#define XDOM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XD_OK 0
+#define XD_ERR_INVALID_ARG (-1)
+#define XD_ERR_HIP (-2)
+#define XD_ERR_WORKSPACE (-3)
+#define XD_ERR_UNSUPPORTED (-4)
+#define XD_ERR_TABLE_FULL (-5)
+#define XD_ERR_INCOMPLETE (-6)
+
+#define XD_MODE_OBLIVIOUS 0
+#define XD_MODE_AWARE 1
+#define XD_MODE_ROTATED 2
+
+#define XD_NUM_XCD 8
+
+/* ------------------------------------------------------------------------------------ */
+/* Library, topology and domain runtime                                                  */
+/* ------------------------------------------------------------------------------------ */
+
+typedef struct {
+    int device;
+    int num_cu;               /* compute units visible to the process            */
+    int num_xcd;              /* XCDs (L2 domains); 8 on MI355X in SPX mode       */
+    int cu_per_xcd;
+    int wave_size;            /* 64 on CDNA                                      */
+    int clock_khz;            /* shader clock                                     */
+    long long l2_bytes;       /* L2 size reported by the runtime (per XCD on CDNA) */
+    long long lds_bytes_per_wg;
+    long long hbm_bytes;
+    char arch[32];            /* e.g. "gfx950:sramecc+:xnack-"                   */
+    char name[96];
+} xd_topology_t;
+
+/* Library version string. */
+const char *xd_version(void);
+
+/* Message describing the last error raised on the calling thread ("" if none). */
+const char *xd_last_error(void);
+
+/* Static description of the device. Replaces the latency-probed SM->side map
+ * latopt::get_map_smid2side (utility/latopt.cuh:487-562): on CDNA the L2 domain of a
+ * workgroup is read from the hardware (HW_REG_XCC_ID), so nothing has to be probed. */
+int xd_topology_query(int device, xd_topology_t *out);
+
+/* DomainScan: launch `num_wg` workgroups and record, for each, the hardware placement
+ * word ((xcc_id << 24) | (se_id << 16) | (sh_id << 12) | (cu_id << 8) | simd_id) into
+ * out_placement[wg] (device buffer of num_wg uint32). Evidence for the workgroup->XCD
+ * dispatch order the XCD-aware kernels assume. Stands in for the reference's SM->side
+ * calibration (utility/get_smid2side.cu:73-112, utility/latopt.cuh:487-530). */
+int xd_domain_scan(int num_wg, uint32_t *out_placement, void *stream);
+
+/* Bytes of read traffic xd_cache_flush needs to evict 8 x 4 MB L2 and the 256 MB
+ * Infinity Cache (>= 4x their sum). */
+size_t xd_cache_flush_bytes(void);
+
+/* Stream-read `bytes` of `buf` (device, >= xd_cache_flush_bytes()) so that previously
+ * touched data is no longer cache resident. Replaces GlobalL2Cache::reset
+ * (utility/latopt.cuh:103-134) and flush_l2_k (histogram256_sideaware.cu:39-49), which
+ * size the flush from cudaDeviceProp::l2CacheSize. */
+int xd_cache_flush(const void *buf, size_t bytes, void *stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* GEMV  y[M] = A[M,K] . x[K], row-major A, fp32 accumulation                            */
+/* ------------------------------------------------------------------------------------ */
+
+/* fp32 GEMV. Replaces gemv_partitioned_kernel / gemv_baseline_kernel
+ * (applications/gemv/src/gemv_k1024_persistent_subwarp.cu:163-231), generalised from the
+ * compile-time K=1024 to any K with K % 4 == 0 and 16-byte aligned A and x.
+ * Writes every y[i] (no accumulation into y). */
+int xd_gemv_f32(const float *A, const float *x, float *y, int M, int K, int mode, void *stream);
+
+/* fp16 weights and vector (IEEE binary16 bit patterns), fp32 accumulation, fp32 y.
+ * Same structure as xd_gemv_f32; K % 8 == 0, 16-byte aligned W and x. */
+int xd_gemv_f16f32(const uint16_t *W, const uint16_t *x, float *y, int M, int K, int mode,
+                   void *stream);
+
+/* ------------------------------------------------------------------------------------ */
+/* Seeded input generators (host). Fully specified integer mixers; no libc RNG.          */
+/* ------------------------------------------------------------------------------------ */
+
+/* splitmix64 output number `index` (0-based) of the stream seeded with `seed`. */
+uint64_t xd_rand64(uint64_t seed, uint64_t index);
+
+/* out[i] = ((xd_rand64(seed, i) >> 40) * 2^-23) - 1, i.e. U[-1,1) on a 2^-23 grid. */
+int xd_gen_uniform_f32(float *out, size_t n, uint64_t seed);
+
+/* out[i] = binary16(RNE) of mean + stddev * N(0,1), Box-Muller over xd_rand64(seed, .). */
+int xd_gen_normal_f16(uint16_t *out, size_t n, double mean, double stddev, uint64_t seed);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XDOM_H */

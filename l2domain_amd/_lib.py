@@ -1,0 +1,96 @@
+"""ctypes binding of libxdom.so (the C ABI declared in include/xdom.h).
+
+The library is loaded from the package directory only. There is no fallback: if the
+shared object is missing or does not export a declared symbol, import fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("XDOM_LIB", PKG / "libxdom.so"))
+
+XD_OK = 0
+XD_ERR_INVALID_ARG = -1
+XD_ERR_HIP = -2
+XD_ERR_WORKSPACE = -3
+XD_ERR_UNSUPPORTED = -4
+XD_ERR_TABLE_FULL = -5
+XD_ERR_INCOMPLETE = -6
+
+MODE_OBLIVIOUS = 0
+MODE_AWARE = 1
+MODE_ROTATED = 2
+MODES = {"oblivious": MODE_OBLIVIOUS, "baseline": MODE_OBLIVIOUS, "aware": MODE_AWARE,
+         "rotated": MODE_ROTATED, "swapped": MODE_ROTATED}
+
+_ERR_NAMES = {XD_ERR_INVALID_ARG: "XD_ERR_INVALID_ARG", XD_ERR_HIP: "XD_ERR_HIP",
+              XD_ERR_WORKSPACE: "XD_ERR_WORKSPACE", XD_ERR_UNSUPPORTED: "XD_ERR_UNSUPPORTED",
+              XD_ERR_TABLE_FULL: "XD_ERR_TABLE_FULL", XD_ERR_INCOMPLETE: "XD_ERR_INCOMPLETE"}
+
+
+class XdomError(RuntimeError):
+    def __init__(self, code: int, fn: str, msg: str):
+        super().__init__(f"{fn} failed with {_ERR_NAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+class Topology(C.Structure):
+    _fields_ = [("device", C.c_int), ("num_cu", C.c_int), ("num_xcd", C.c_int),
+                ("cu_per_xcd", C.c_int), ("wave_size", C.c_int), ("clock_khz", C.c_int),
+                ("l2_bytes", C.c_longlong), ("lds_bytes_per_wg", C.c_longlong),
+                ("hbm_bytes", C.c_longlong), ("arch", C.c_char * 32), ("name", C.c_char * 96)]
+
+
+VP = C.c_void_p
+SZ = C.c_size_t
+I = C.c_int
+U32 = C.c_uint32
+U64 = C.c_uint64
+I64 = C.c_int64
+D = C.c_double
+
+# name -> (restype, argtypes). Kept in the order of include/xdom.h.
+SIGNATURES: dict[str, tuple] = {
+    "xd_version": (C.c_char_p, []),
+    "xd_last_error": (C.c_char_p, []),
+    "xd_topology_query": (I, [I, C.POINTER(Topology)]),
+    "xd_domain_scan": (I, [I, VP, VP]),
+    "xd_cache_flush_bytes": (SZ, []),
+    "xd_cache_flush": (I, [VP, SZ, VP]),
+    "xd_gemv_f32": (I, [VP, VP, VP, I, I, I, VP]),
+    "xd_gemv_f16f32": (I, [VP, VP, VP, I, I, I, VP]),
+    "xd_rand64": (U64, [U64, U64]),
+    "xd_gen_uniform_f32": (I, [VP, SZ, U64]),
+    "xd_gen_normal_f16": (I, [VP, SZ, D, D, U64]),
+}
+
+
+def _load() -> C.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"libxdom.so not found at {LIB_PATH}; build it first with `python -m l2domain_amd.build` "
+            "(there is no CPU fallback for the XCD-domain kernels)")
+    lib = C.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError here means the .so is stale
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def check(code: int, fn: str) -> None:
+    if code != XD_OK:
+        raise XdomError(code, fn, lib.xd_last_error().decode(errors="replace"))
+
+
+def call(name: str, *args):
+    """Calls an int-returning entry point and raises XdomError on a non-zero status."""
+    rc = getattr(lib, name)(*args)
+    check(rc, name)
+    return rc

@@ -1,0 +1,128 @@
+// Shared device and host helpers of libxdom (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "xdom.h"
+
+namespace xd {
+
+constexpr int kNumXcd = XD_NUM_XCD;
+constexpr int kWave = 64;
+
+// Native 16-byte vector (usable with the nontemporal builtins, unlike HIP's uint4 class).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------------------
+// Error reporting (host)
+// ---------------------------------------------------------------------------------------
+void set_error(const std::string &msg);
+int fail(int code, const std::string &msg);
+int hip_fail(hipError_t e, const char *what);
+
+#define XD_HIP(call)                                          \
+    do {                                                      \
+        hipError_t xd_e_ = (call);                            \
+        if (xd_e_ != hipSuccess) return ::xd::hip_fail(xd_e_, #call); \
+    } while (0)
+
+#define XD_REQUIRE(cond, msg)                                              \
+    do {                                                                   \
+        if (!(cond)) return ::xd::fail(XD_ERR_INVALID_ARG, (msg));         \
+    } while (0)
+
+// Checks the launch that was just enqueued.
+inline int launch_status(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, what);
+    return XD_OK;
+}
+
+// Per-device pass counter used by XD_MODE_ROTATED (advances once per pass).
+unsigned next_rotation(int passes);
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------------------
+// Hardware placement (device)
+// ---------------------------------------------------------------------------------------
+
+// XCD (accelerator complex die) the calling wave runs on, read from HW_REG_XCC_ID.
+__device__ __forceinline__ uint32_t hw_xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xfu;
+}
+
+// Raw HW_REG_HW_ID word: SIMD [5:4], CU [11:8], SH [12], SE [15:13] on GFX9.
+__device__ __forceinline__ uint32_t hw_id_word() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(v));
+    return v;
+}
+
+// Logical placement of workgroup `wg` in a grid whose size is a multiple of 8, under the
+// round-robin workgroup -> XCD dispatch of CDNA3/4 in SPX mode (wg i runs on XCD i mod 8,
+// verified by xd_domain_scan). `slice` is the data slice this workgroup serves.
+struct XcdSlot {
+    int slice;    // which 1/8 of the data
+    int rank;     // workgroup index within the XCD
+    int per_xcd;  // workgroups per XCD
+};
+
+__device__ __forceinline__ XcdSlot xcd_slot(int wg, int grid, int mode, unsigned rot) {
+    XcdSlot s;
+    s.per_xcd = grid / kNumXcd;
+    s.rank = wg / kNumXcd;
+    int xcd = wg % kNumXcd;
+    s.slice = (mode == XD_MODE_ROTATED) ? (int)((xcd + rot) % kNumXcd) : xcd;
+    return s;
+}
+
+// ---------------------------------------------------------------------------------------
+// Wave64 reductions via DPP (GFX9 row/bank broadcast sequence). Result in every lane.
+// ---------------------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp_f32(float v) {
+    // Lanes outside the row mask receive 0.0f (old value), the identity of the sum.
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 ROW_MASK, BANK_MASK, false));
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+    v += dpp_f32<0xb1>(v);         // quad_perm [1,0,3,2]
+    v += dpp_f32<0x4e>(v);         // quad_perm [2,3,0,1]
+    v += dpp_f32<0x141>(v);        // row_half_mirror
+    v += dpp_f32<0x140>(v);        // row_mirror: each row of 16 holds its sum
+    v += dpp_f32<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+    v += dpp_f32<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3: lane 63 holds the total
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+    v += dpp_u32<0xb1>(v);
+    v += dpp_u32<0x4e>(v);
+    v += dpp_u32<0x141>(v);
+    v += dpp_u32<0x140>(v);
+    v += dpp_u32<0x142, 0xa>(v);
+    v += dpp_u32<0x143, 0xc>(v);
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+// Number of active lanes below the calling lane in a 64-bit ballot mask.
+__device__ __forceinline__ uint32_t mask_rank(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+}  // namespace xd

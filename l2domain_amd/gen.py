@@ -1,0 +1,37 @@
+"""Seeded input generators (host side, in libxdom). Fully specified: see include/xdom.h."""
+from __future__ import annotations
+
+import numpy as np
+
+from . import _lib
+
+SEED_GEMV_F32 = 4242      # applications/gemv/run.sh:80 passes seed 4242
+SEED_GEMV_F16_W = 4243
+SEED_GEMV_F16_X = 4244
+X_SEED_OFFSET = 0x9E37    # x uses seed + 0x9e37, as init_data does (GEMV.cu:129)
+
+
+def rand64(seed: int, index: int) -> int:
+    return int(_lib.lib.xd_rand64(seed, index))
+
+
+def uniform_f32(n: int, seed: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _lib.call("xd_gen_uniform_f32", out.ctypes.data, n, seed)
+    return out
+
+
+def normal_f16(n: int, mean: float, stddev: float, seed: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    _lib.call("xd_gen_normal_f16", out.ctypes.data, n, mean, stddev, seed)
+    return out.view(np.float16)
+
+
+def gemv_f32_inputs(M: int, K: int, seed: int = SEED_GEMV_F32):
+    """A[M,K], x[K]: U[-1,1) on a 2^-23 grid (configs[0] of the build)."""
+    return uniform_f32(M * K, seed).reshape(M, K), uniform_f32(K, seed + X_SEED_OFFSET)
+
+
+def gemv_f16_inputs(M: int, K: int, w_seed: int = SEED_GEMV_F16_W, x_seed: int = SEED_GEMV_F16_X):
+    """W[M,K] ~ N(0, 0.02), x[K] ~ N(0, 1), both rounded to binary16."""
+    return normal_f16(M * K, 0.0, 0.02, w_seed).reshape(M, K), normal_f16(K, 0.0, 1.0, x_seed)

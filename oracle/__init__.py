@@ -1,0 +1,99 @@
+"""CPU oracle for the XCD-domain kernels -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this
+package, and only as the checker or the timed CPU baseline. The product never does.
+The functions restate the reference's CPU verification loops (cited in oracle.c).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+
+def _load() -> C.CDLL:
+    if not LIB_PATH.exists():
+        subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return C.CDLL(str(LIB_PATH))
+
+
+lib = _load()
+VP, SZ, I, I64, U64, U32, U16, D = (C.c_void_p, C.c_size_t, C.c_int, C.c_int64, C.c_uint64, C.c_uint32,
+                                    C.c_uint16, C.c_double)
+_SIGS = {
+    "ora_splitmix64": (U64, [U64, U64]),
+    "ora_mix32": (U32, [U32]),
+    "ora_f64_to_f16": (U16, [D]),
+    "ora_f16_to_f64": (D, [U16]),
+    "ora_gen_uniform_f32": (None, [VP, SZ, U64]),
+    "ora_gen_normal_f16": (None, [VP, SZ, D, D, U64]),
+    "ora_gemv_f32_seq": (None, [VP, VP, VP, I64, I64, I]),
+    "ora_gemv_f32_f64": (None, [VP, VP, VP, VP, I64, I64, I]),
+    "ora_gemv_f16_f64": (None, [VP, VP, VP, VP, I64, I64, I]),
+}
+for _n, (_r, _a) in _SIGS.items():
+    _f = getattr(lib, _n)
+    _f.restype = _r
+    _f.argtypes = _a
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def splitmix64(seed: int, index: int) -> int:
+    return int(lib.ora_splitmix64(seed, index))
+
+
+def mix32(x: int) -> int:
+    return int(lib.ora_mix32(x))
+
+
+def f64_to_f16_bits(d: float) -> int:
+    return int(lib.ora_f64_to_f16(d))
+
+
+def uniform_f32(n: int, seed: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib.ora_gen_uniform_f32(_p(out), n, seed)
+    return out
+
+
+def normal_f16(n: int, mean: float, stddev: float, seed: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    lib.ora_gen_normal_f16(_p(out), n, mean, stddev, seed)
+    return out.view(np.float16)
+
+
+def gemv_f32_seq(A: np.ndarray, x: np.ndarray, nthreads: int = 1) -> np.ndarray:
+    """GEMV.cu:383-390: float running sum, k ascending."""
+    A = np.ascontiguousarray(A, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = A.shape
+    y = np.empty(M, dtype=np.float32)
+    lib.ora_gemv_f32_seq(_p(A), _p(x), _p(y), M, K, nthreads)
+    return y
+
+
+def gemv_f64(A: np.ndarray, x: np.ndarray, nthreads: int = 1):
+    """Returns (y, yabs) in float64: y = A.x, yabs[i] = sum_k |A_ik x_k|."""
+    M, K = A.shape
+    y = np.empty(M, dtype=np.float64)
+    yabs = np.empty(M, dtype=np.float64)
+    if A.dtype == np.float32:
+        A = np.ascontiguousarray(A)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        lib.ora_gemv_f32_f64(_p(A), _p(x), _p(y), _p(yabs), M, K, nthreads)
+    elif A.dtype == np.float16:
+        A = np.ascontiguousarray(A).view(np.uint16)
+        x = np.ascontiguousarray(x, dtype=np.float16).view(np.uint16)
+        lib.ora_gemv_f16_f64(_p(A), _p(x), _p(y), _p(yabs), M, K, nthreads)
+    else:
+        raise TypeError(A.dtype)
+    return y, yabs

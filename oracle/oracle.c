@@ -1,0 +1,208 @@
+/*
+ * oracle.c -- CPU oracle for the XCD-domain kernels. TEST INFRASTRUCTURE ONLY: loaded by
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg; never by the product.
+ *
+ * Pinning (what checks each function against something other than itself) is listed in
+ * tests/test_oracle.py; a function without such a check is marked "parity unpinned" here.
+ */
+#define _GNU_SOURCE
+#include "oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------------------ */
+/* threading helper                                                                      */
+/* ------------------------------------------------------------------------------------ */
+typedef void (*range_fn)(void *ctx, int64_t begin, int64_t end);
+typedef struct {
+    range_fn fn;
+    void *ctx;
+    int64_t b, e;
+} range_job;
+
+static void *range_tramp(void *p) {
+    range_job *j = (range_job *)p;
+    j->fn(j->ctx, j->b, j->e);
+    return NULL;
+}
+
+static void parallel_range(int64_t n, int nthreads, range_fn fn, void *ctx) {
+    if (nthreads <= 1 || n < 2) {
+        fn(ctx, 0, n);
+        return;
+    }
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    range_job jobs[256];
+    int64_t per = (n + nthreads - 1) / nthreads;
+    int started = 0;
+    for (int t = 0; t < nthreads; ++t) {
+        int64_t b = (int64_t)t * per, e = b + per < n ? b + per : n;
+        if (b >= e) break;
+        jobs[t].fn = fn;
+        jobs[t].ctx = ctx;
+        jobs[t].b = b;
+        jobs[t].e = e;
+        if (pthread_create(&th[t], NULL, range_tramp, &jobs[t]) != 0) {
+            fn(ctx, b, e);
+            continue;
+        }
+        started = t + 1;
+    }
+    for (int t = 0; t < started; ++t) pthread_join(th[t], NULL);
+}
+
+/* ------------------------------------------------------------------------------------ */
+/* generators                                                                            */
+/* ------------------------------------------------------------------------------------ */
+
+/* splitmix64 (Steele, Lea, Flood 2014): state += 0x9e3779b97f4a7c15, then the variant-13
+ * output mix. Output number `index` of the stream whose initial state is `seed`. */
+uint64_t ora_splitmix64(uint64_t seed, uint64_t index) {
+    uint64_t z = seed + (index + 1) * 0x9e3779b97f4a7c15ULL;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+
+/* GEMV.cu:56-63 (also HIST.cu:333-338, HASH.cu:29-36). */
+uint32_t ora_mix32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+/* binary64 -> binary16, round to nearest even, by integer manipulation of the bits. */
+uint16_t ora_f64_to_f16(double d) {
+    uint64_t b;
+    memcpy(&b, &d, 8);
+    uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+    uint64_t E = (b >> 52) & 0x7ffu;
+    uint64_t m = b & 0xfffffffffffffULL;
+    if (E == 0x7ff) return (uint16_t)(sign | (m ? 0x7e00u : 0x7c00u));
+    if (E == 0) return sign; /* zero or binary64 subnormal: far below 2^-25 */
+    int64_t e = (int64_t)E - 1023;
+    if (e > 15) return (uint16_t)(sign | 0x7c00u);
+    if (e >= -14) {
+        uint64_t hm = m >> 42, rem = m & ((1ULL << 42) - 1), half = 1ULL << 41;
+        uint32_t r = (uint32_t)(((uint64_t)(e + 15) << 10) | hm);
+        if (rem > half || (rem == half && (hm & 1))) ++r; /* carries into exponent / inf */
+        return (uint16_t)(sign | r);
+    }
+    uint64_t M = (1ULL << 52) | m;
+    int64_t shift = 42 + (-14 - e);
+    if (shift >= 54) return sign;
+    uint64_t q = M >> shift, rem = M & ((1ULL << shift) - 1), half = 1ULL << (shift - 1);
+    if (rem > half || (rem == half && (q & 1))) ++q;
+    return (uint16_t)(sign | (uint16_t)q);
+}
+
+double ora_f16_to_f64(uint16_t h) {
+    int s = (h >> 15) & 1, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    double v;
+    if (e == 0) v = ldexp((double)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = ldexp((double)(m | 0x400), e - 25);
+    return s ? -v : v;
+}
+
+void ora_gen_uniform_f32(float *out, size_t n, uint64_t seed) {
+    for (size_t i = 0; i < n; ++i) {
+        int32_t k = (int32_t)(ora_splitmix64(seed, i) >> 40) - (1 << 23);
+        out[i] = (float)ldexp((double)k, -23);
+    }
+}
+
+void ora_gen_normal_f16(uint16_t *out, size_t n, double mean, double stddev, uint64_t seed) {
+    const double two_pi = 2.0 * 3.14159265358979323846264338327950288;
+    for (size_t j = 0; 2 * j < n; ++j) {
+        double u1 = ldexp((double)((ora_splitmix64(seed, 2 * j) >> 11) + 1), -53);
+        double u2 = ldexp((double)(ora_splitmix64(seed, 2 * j + 1) >> 11), -53);
+        double r = sqrt(-2.0 * log(u1));
+        out[2 * j] = ora_f64_to_f16(mean + stddev * (r * cos(two_pi * u2)));
+        if (2 * j + 1 < n) out[2 * j + 1] = ora_f64_to_f16(mean + stddev * (r * sin(two_pi * u2)));
+    }
+}
+
+/* ------------------------------------------------------------------------------------ */
+/* GEMV                                                                                  */
+/* ------------------------------------------------------------------------------------ */
+typedef struct {
+    const void *A, *x;
+    float *yf;
+    double *yd, *yabs;
+    int64_t K;
+} gemv_ctx;
+
+/* GEMV.cu:383-390: sum += a[k] * x[k] in float, k ascending. */
+static void gemv_seq_rows(void *p, int64_t b, int64_t e) {
+    gemv_ctx *c = (gemv_ctx *)p;
+    const float *A = (const float *)c->A, *x = (const float *)c->x;
+    for (int64_t r = b; r < e; ++r) {
+        float sum = 0.0f;
+        const float *a = A + r * c->K;
+        for (int64_t k = 0; k < c->K; ++k) {
+            float prod = a[k] * x[k];
+            sum = sum + prod;
+        }
+        c->yf[r] = sum;
+    }
+}
+
+static void gemv_f64_rows(void *p, int64_t b, int64_t e) {
+    gemv_ctx *c = (gemv_ctx *)p;
+    const float *A = (const float *)c->A, *x = (const float *)c->x;
+    for (int64_t r = b; r < e; ++r) {
+        double s = 0.0, sa = 0.0;
+        const float *a = A + r * c->K;
+        for (int64_t k = 0; k < c->K; ++k) {
+            double t = (double)a[k] * (double)x[k];
+            s += t;
+            sa += fabs(t);
+        }
+        c->yd[r] = s;
+        if (c->yabs) c->yabs[r] = sa;
+    }
+}
+
+static void gemv_f16_rows(void *p, int64_t b, int64_t e) {
+    gemv_ctx *c = (gemv_ctx *)p;
+    const uint16_t *W = (const uint16_t *)c->A, *x = (const uint16_t *)c->x;
+    double *xd = (double *)malloc(sizeof(double) * (size_t)c->K);
+    for (int64_t k = 0; k < c->K; ++k) xd[k] = ora_f16_to_f64(x[k]);
+    for (int64_t r = b; r < e; ++r) {
+        double s = 0.0, sa = 0.0;
+        const uint16_t *w = W + r * c->K;
+        for (int64_t k = 0; k < c->K; ++k) {
+            double t = ora_f16_to_f64(w[k]) * xd[k];
+            s += t;
+            sa += fabs(t);
+        }
+        c->yd[r] = s;
+        if (c->yabs) c->yabs[r] = sa;
+    }
+    free(xd);
+}
+
+void ora_gemv_f32_seq(const float *A, const float *x, float *y, int64_t M, int64_t K, int nthreads) {
+    gemv_ctx c = {A, x, y, NULL, NULL, K};
+    parallel_range(M, nthreads, gemv_seq_rows, &c);
+}
+
+void ora_gemv_f32_f64(const float *A, const float *x, double *y, double *yabs, int64_t M, int64_t K,
+                      int nthreads) {
+    gemv_ctx c = {A, x, NULL, y, yabs, K};
+    parallel_range(M, nthreads, gemv_f64_rows, &c);
+}
+
+void ora_gemv_f16_f64(const uint16_t *W, const uint16_t *x, double *y, double *yabs, int64_t M,
+                      int64_t K, int nthreads) {
+    gemv_ctx c = {W, x, NULL, y, yabs, K};
+    parallel_range(M, nthreads, gemv_f16_rows, &c);
+}

@@ -1,0 +1,33 @@
+/*
+ * oracle.h -- CPU restatement of the reference's verification paths.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker (or the timed CPU
+ * baseline). The product (libxdom, its runners and Python mirror) never links or calls it.
+ *
+ * Each function cites the reference code whose behaviour it restates.
+ */
+#ifndef XDOM_ORACLE_H
+#define XDOM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+/* ---- generators (independent restatement of the build's seeded inputs) ---- */
+uint64_t ora_splitmix64(uint64_t seed, uint64_t index);
+uint32_t ora_mix32(uint32_t x); /* lowbias32 finaliser, GEMV.cu:56-63 */
+uint16_t ora_f64_to_f16(double d);
+double ora_f16_to_f64(uint16_t h);
+void ora_gen_uniform_f32(float *out, size_t n, uint64_t seed);
+void ora_gen_normal_f16(uint16_t *out, size_t n, double mean, double stddev, uint64_t seed);
+
+/* ---- GEMV (GEMV.cu:383-402) ---- */
+/* The reference's own check: fp32 running sum in k order. */
+void ora_gemv_f32_seq(const float *A, const float *x, float *y, int64_t M, int64_t K, int nthreads);
+/* fp64-accumulated y and the per-row magnitude sum |A_ik * x_k| (for relative bounds). */
+void ora_gemv_f32_f64(const float *A, const float *x, double *y, double *yabs, int64_t M, int64_t K,
+                      int nthreads);
+void ora_gemv_f16_f64(const uint16_t *W, const uint16_t *x, double *y, double *yabs, int64_t M,
+                      int64_t K, int nthreads);
+
+#endif

@@ -1,0 +1,33 @@
+"""The product's seeded generators (libxdom host code) equal the oracle's independent
+restatement bit for bit, so GPU inputs are exactly what the CPU checks use."""
+import numpy as np
+
+import oracle as ora
+from l2domain_amd import gen
+
+
+def test_rand64_matches_oracle():
+    for s in (0, 42, 4242, 2**64 - 1):
+        for i in (0, 1, 2, 12345, 2**40):
+            assert gen.rand64(s, i) == ora.splitmix64(s, i)
+
+
+def test_uniform_f32_matches_oracle():
+    n = (1 << 17) + 3  # crosses the threaded split
+    np.testing.assert_array_equal(gen.uniform_f32(n, 4242).view(np.uint32),
+                                  ora.uniform_f32(n, 4242).view(np.uint32))
+
+
+def test_normal_f16_matches_oracle():
+    n = (1 << 17) + 1  # odd length: last element uses only the cosine branch
+    for mean, sd, seed in ((0.0, 0.02, 4243), (0.0, 1.0, 4244), (3.0, 1e-6, 9)):
+        np.testing.assert_array_equal(gen.normal_f16(n, mean, sd, seed).view(np.uint16),
+                                      ora.normal_f16(n, mean, sd, seed).view(np.uint16))
+
+
+def test_gemv_inputs_shapes_and_seeds():
+    A, x = gen.gemv_f32_inputs(8, 16)
+    assert A.shape == (8, 16) and x.shape == (16,)
+    np.testing.assert_array_equal(x, ora.uniform_f32(16, 4242 + 0x9E37))
+    W, xh = gen.gemv_f16_inputs(4, 8)
+    assert W.dtype == np.float16 and xh.dtype == np.float16

@@ -1,0 +1,113 @@
+"""GEMV parity on the GPU: libxdom (through the C ABI) against the CPU oracle.
+
+Tolerances: fp32 inputs 1e-3 relative, fp16 inputs with fp32
+accumulation 2e-2 relative; relative = max_i |y_i - ref_i| / max_i |ref_i| with ref the
+fp64-accumulated oracle. Also checked: the reference's own pass rule (max |y - y_seq| <= 1e-3
+against its fp32 sequential loop, applications/gemv/run.sh:94-97) and an exact mode with
+small-integer inputs, where every summation order gives the same fp32 result.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as ora
+from l2domain_amd import gen
+from l2domain_amd.gemv import gemv
+
+pytestmark = pytest.mark.gpu
+MODES = ["oblivious", "aware", "rotated"]
+
+
+def run(A: np.ndarray, x: np.ndarray, mode) -> np.ndarray:
+    dA = torch.from_numpy(np.ascontiguousarray(A)).cuda()
+    dx = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+    y = torch.full((A.shape[0],), float("nan"), dtype=torch.float32, device="cuda")
+    gemv(dA, dx, y, mode=mode)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def rel_err(y, ref):
+    return float(np.max(np.abs(y.astype(np.float64) - ref)) / max(np.max(np.abs(ref)), 1e-300))
+
+
+@pytest.fixture(scope="module")
+def f32_config():
+    A, x = gen.gemv_f32_inputs(4096, 4096)
+    ref, yabs = ora.gemv_f64(A, x, nthreads=8)
+    seq = ora.gemv_f32_seq(A, x, nthreads=8)
+    return A, x, ref, yabs, seq
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_f32_4096_config(f32_config, mode):
+    A, x, ref, yabs, seq = f32_config
+    y = run(A, x, mode)
+    assert np.all(np.isfinite(y))
+    assert rel_err(y, ref) <= 1e-3
+    # element-wise bound: fp32 accumulation error is far below 1e-3 of sum |a x|
+    assert np.all(np.abs(y - ref) <= 1e-3 * yabs)
+    assert float(np.max(np.abs(y - seq))) <= 1e-3  # the reference's max_abs_error rule
+
+
+def test_f32_modes_bit_identical(f32_config):
+    A, x, *_ = f32_config
+    ys = [run(A, x, m) for m in MODES]
+    for y in ys[1:]:
+        np.testing.assert_array_equal(ys[0].view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_f32_integer_inputs_exact(mode):
+    rng = np.random.default_rng(1234)
+    A = rng.integers(-8, 9, size=(4096, 4096)).astype(np.float32)
+    x = rng.integers(-3, 4, size=4096).astype(np.float32)
+    y = run(A, x, mode)
+    np.testing.assert_array_equal(y, ora.gemv_f32_seq(A, x, nthreads=8))
+
+
+@pytest.mark.parametrize("M,K", [(1, 4), (7, 12), (9, 256), (1000, 4100), (4097, 64), (33, 16384)])
+@pytest.mark.parametrize("mode", ["oblivious", "aware"])
+def test_f32_ragged_shapes(M, K, mode):
+    A, x = gen.gemv_f32_inputs(M, K, seed=M * 7 + K)
+    ref, yabs = ora.gemv_f64(A, x)
+    y = run(A, x, mode)
+    assert rel_err(y, ref) <= 1e-3
+    assert np.all(np.abs(y - ref) <= 1e-3 * yabs + 1e-30)
+
+
+@pytest.fixture(scope="module", params=[(14336, 4096), (4096, 14336)], ids=["up", "down"])
+def f16_config(request):
+    M, K = request.param
+    W, x = gen.gemv_f16_inputs(M, K)
+    ref, yabs = ora.gemv_f64(W, x, nthreads=8)
+    return W, x, ref, yabs
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_f16_decode_shapes(f16_config, mode):
+    W, x, ref, yabs = f16_config
+    y = run(W, x, mode)
+    assert np.all(np.isfinite(y))
+    assert rel_err(y, ref) <= 2e-2
+    assert np.all(np.abs(y - ref) <= 2e-2 * yabs)
+
+
+@pytest.mark.parametrize("M,K", [(1, 8), (3, 24), (100, 1000), (4095, 4104)])
+def test_f16_ragged_shapes(M, K):
+    W, x = gen.gemv_f16_inputs(M, K, w_seed=M, x_seed=K)
+    ref, yabs = ora.gemv_f64(W, x)
+    for mode in MODES:
+        y = run(W, x, mode)
+        assert rel_err(y, ref) <= 2e-2
+        assert np.all(np.abs(y - ref) <= 2e-2 * yabs + 1e-30)
+
+
+def test_f16_integer_inputs_exact():
+    # Integers |w| <= 8, |x| <= 3 are exact in binary16; K=4096 sums stay below 2^24.
+    rng = np.random.default_rng(99)
+    W = rng.integers(-8, 9, size=(512, 4096)).astype(np.float16)
+    x = rng.integers(-3, 4, size=4096).astype(np.float16)
+    ref = (W.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)
+    for mode in MODES:
+        np.testing.assert_array_equal(run(W, x, mode), ref)

@@ -1,0 +1,120 @@
+"""Pins the CPU oracle (oracle/) against published vectors, library routines and closed forms.
+
+Nothing here retypes the oracle's formula: every check compares it with an independent
+source (published known-answer vectors, numpy's own conversion/BLAS, exact integer
+arithmetic, or brute force), chosen so that a dropped term, wrong sign/index or a
+transposed operand fails.
+"""
+import numpy as np
+import pytest
+
+import oracle as ora
+
+# Published splitmix64 outputs for seed 0 (Vigna's splitmix64.c reference / xoshiro seeding).
+SPLITMIX64_SEED0 = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F,
+                    0xF88BB8A8724C81EC, 0x1B39896A51A8749B]
+
+
+def test_splitmix64_published_vectors():
+    assert [ora.splitmix64(0, i) for i in range(5)] == SPLITMIX64_SEED0
+
+
+def test_splitmix64_is_a_stream_of_the_seed():
+    # Output i of seed s equals output 0 of seed s + i*gamma (counter-based definition).
+    g = 0x9E3779B97F4A7C15
+    for s in (1, 4242, 2**63 + 5):
+        for i in (0, 1, 17, 10**9):
+            assert ora.splitmix64(s, i) == ora.splitmix64((s + i * g) % 2**64, 0)
+
+
+def test_mix32_known_answers():
+    # lowbias32 finaliser of GEMV.cu:56-63; values computed independently (SURVEY 8(a) KATs).
+    kat = {0: 0, 1: 0x688990C0, 2: 0xD1132181, 4242: 0xE0D78B3B, 0xFFFFFFFF: 0x6768824A}
+    for k, v in kat.items():
+        assert ora.mix32(k) == v
+
+
+def _f16_cases():
+    rng = np.random.default_rng(7)
+    vals = list(rng.normal(0, 0.02, 20000)) + list(rng.normal(0, 1, 20000))
+    vals += list(rng.uniform(-70000, 70000, 2000)) + list(rng.uniform(-1e-7, 1e-7, 5000))
+    # exact ties, subnormal boundary, overflow boundary, signed zero, specials
+    ulp = 2.0 ** -10
+    vals += [1 + ulp / 2, 1 + 3 * ulp / 2, -(1 + ulp / 2), 2.0 ** -24 / 2, 3 * 2.0 ** -24 / 2,
+             2.0 ** -14, 2.0 ** -14 * (1 - 2 ** -11), 65504.0, 65519.99, 65520.0, 1e300, -0.0, 0.0,
+             2.0 ** -25, 2.0 ** -25 * 1.0000001, 5e-324, float("inf"), float("-inf")]
+    return np.array(vals, dtype=np.float64)
+
+
+def test_f64_to_f16_matches_numpy():
+    vals = _f16_cases()
+    ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([ora.f64_to_f16_bits(float(v)) for v in vals], dtype=np.uint16)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_uniform_f32_grid_and_range():
+    a = ora.uniform_f32(1 << 16, 4242)
+    assert a.min() >= -1.0 and a.max() < 1.0
+    k = a.astype(np.float64) * 2.0 ** 23
+    assert np.all(k == np.round(k))  # on the 2^-23 grid
+    # The 24-bit integer is the top bits of the splitmix64 output.
+    for i in (0, 1, 999):
+        assert a[i] == (ora.splitmix64(4242, i) >> 40) * 2.0 ** -23 - 1.0
+    assert abs(a.mean()) < 0.01 and abs(a.var() - 1 / 3) < 0.01
+
+
+def test_normal_f16_moments():
+    a = ora.normal_f16(1 << 18, 0.0, 0.02, 4243).astype(np.float64)
+    assert abs(a.mean()) < 2e-4
+    assert abs(a.std() - 0.02) < 2e-4
+    # Box-Muller tail: about 4.55% beyond 2 sigma.
+    assert abs(np.mean(np.abs(a) > 0.04) - 0.0455) < 0.003
+
+
+@pytest.mark.parametrize("M,K", [(1, 4), (7, 12), (33, 256), (64, 1000)])
+def test_gemv_integer_inputs_exact(M, K):
+    # Small integers give exact fp32 and fp64 sums (INTEGER_FLOAT_INPUTS idea, GEMV.cu:122-134):
+    # both oracle loops must equal numpy's integer matmul exactly. M != K catches a transposition.
+    rng = np.random.default_rng(M * 1000 + K)
+    Ai = rng.integers(-8, 9, size=(M, K))
+    xi = rng.integers(-3, 4, size=K)
+    ref = Ai @ xi
+    A = Ai.astype(np.float32)
+    x = xi.astype(np.float32)
+    np.testing.assert_array_equal(ora.gemv_f32_seq(A, x), ref.astype(np.float32))
+    y, yabs = ora.gemv_f64(A, x)
+    np.testing.assert_array_equal(y, ref.astype(np.float64))
+    np.testing.assert_array_equal(yabs, (np.abs(Ai) @ np.abs(xi)).astype(np.float64))
+
+
+def test_gemv_f64_matches_numpy_blas():
+    rng = np.random.default_rng(3)
+    A = rng.uniform(-1, 1, (129, 513)).astype(np.float32)
+    x = rng.uniform(-1, 1, 513).astype(np.float32)
+    y, _ = ora.gemv_f64(A, x, nthreads=4)
+    ref = A.astype(np.float64) @ x.astype(np.float64)
+    np.testing.assert_allclose(y, ref, rtol=0, atol=1e-12)
+
+
+def test_gemv_f32_seq_is_sequential_float():
+    # Brute force restatement with numpy float32 scalars, k ascending.
+    rng = np.random.default_rng(5)
+    A = rng.uniform(-1, 1, (3, 300)).astype(np.float32)
+    x = rng.uniform(-1, 1, 300).astype(np.float32)
+    ref = []
+    for r in range(3):
+        s = np.float32(0)
+        for k in range(300):
+            s = np.float32(s + np.float32(A[r, k] * x[k]))
+        ref.append(s)
+    np.testing.assert_array_equal(ora.gemv_f32_seq(A, x), np.array(ref, dtype=np.float32))
+
+
+def test_gemv_f16_uses_half_values():
+    rng = np.random.default_rng(11)
+    W = rng.normal(0, 0.02, (17, 64)).astype(np.float16)
+    x = rng.normal(0, 1, 64).astype(np.float16)
+    y, _ = ora.gemv_f64(W, x)
+    ref = W.astype(np.float64) @ x.astype(np.float64)
+    np.testing.assert_allclose(y, ref, rtol=0, atol=1e-13)

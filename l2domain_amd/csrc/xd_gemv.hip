@@ -11,6 +11,8 @@
 // (oblivious). No MFMA: GEMV is 0.5 (fp32) or 1 (fp16) flop per byte of A.
 #include <hip/hip_runtime.h>
 
+#include <stdlib.h>
+
 #include "xd_common.hpp"
 
 namespace xd {
@@ -82,7 +84,102 @@ gemv_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__r
     }
 }
 
+// Exact-width variant: each row is split into S segments of 64*CW vectors, one wave per
+// segment, so every lane owns exactly CW vectors and no load needs a bounds check. The
+// first row's loads are issued before x is staged in LDS, so the x round trip overlaps the
+// A stream; with DB the wave's next row is loaded while the current one is reduced.
+// Partial sums of a split row meet in LDS.
+template <bool F16, int CW, int S, bool DB>
+__global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4)))
+gemv_exact_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__restrict__ y, int M,
+                  int rows_per_wg, int nchunks, int mode, unsigned rot) {
+    constexpr int nv = kWave * CW * S;
+    constexpr int kRowsPerPass = kGemvWaves / S;
+    extern __shared__ uint4 xs[];
+    __shared__ float part[kGemvWaves];
+    const int b = (int)blockIdx.x;
+    int chunk;
+    if (mode == XD_MODE_OBLIVIOUS) {
+        chunk = b;
+    } else {
+        XcdSlot sl = xcd_slot(b, (int)gridDim.x, mode, rot);
+        chunk = sl.slice * sl.per_xcd + sl.rank;
+    }
+    if (chunk >= nchunks) return;
+    const int r0 = chunk * rows_per_wg;
+    const int r1 = min(M, r0 + rows_per_wg);
+    const int wave = (int)threadIdx.x / kWave;
+    const int lane = (int)threadIdx.x % kWave;
+    const int slot = wave / S;                  // row within a pass
+    const int seg = wave % S;                   // segment of that row
+    const int voff = seg * (kWave * CW) + lane; // first vector of this lane in a row
+
+    int row = r0 + slot;
+    uint4 a[CW];
+    if (row < r1) {
+        const uint4 *p = A + (size_t)row * nv + voff;
+#pragma unroll
+        for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
+    }
+    for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
+    __syncthreads();
+
+    // Every wave runs the same number of passes so that the LDS combine barrier is uniform.
+    for (int base = r0; base < r1; base += kRowsPerPass) {
+        row = base + slot;
+        const int next = row + kRowsPerPass;
+        const bool live = row < r1;
+        uint4 nb[DB ? CW : 1];
+        if (DB && next < r1) {
+            const uint4 *p = A + (size_t)next * nv + voff;
+#pragma unroll
+            for (int u = 0; u < (DB ? CW : 1); ++u) nb[u] = p[u * kWave];
+        }
+        float acc0 = 0.0f, acc1 = 0.0f;
+        if (live) {
+#pragma unroll
+            for (int u = 0; u < CW; u += 2) {
+                const uint4 xv0 = xs[voff + u * kWave];
+                acc0 = F16 ? dot16_f16(a[u], xv0, acc0) : dot16_f32(a[u], xv0, acc0);
+                if (u + 1 < CW) {
+                    const uint4 xv1 = xs[voff + (u + 1) * kWave];
+                    acc1 = F16 ? dot16_f16(a[u + 1], xv1, acc1) : dot16_f32(a[u + 1], xv1, acc1);
+                }
+            }
+        }
+        const float acc = wave_sum_f32(acc0 + acc1);
+        if (S == 1) {
+            if (live && lane == 0) y[row] = acc;
+        } else {
+            if (lane == 0) part[wave] = acc;
+            __syncthreads();
+            if (live && seg == 0 && lane == 0) {
+                float t = part[wave];
+#pragma unroll
+                for (int k = 1; k < S; ++k) t += part[wave + k];
+                y[row] = t;
+            }
+            __syncthreads();
+        }
+        if (next < r1) {
+            if (DB) {
+#pragma unroll
+                for (int u = 0; u < (DB ? CW : 1); ++u) a[u] = nb[u];
+            } else {
+                const uint4 *p = A + (size_t)next * nv + voff;
+#pragma unroll
+                for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
+            }
+        }
+    }
+}
+
 static int rows_per_workgroup(int M, int nv) {
+    // XD_GEMV_ROWS_PER_WG overrides the heuristic (tuning sweeps); must be a multiple of 4.
+    if (const char *e = getenv("XD_GEMV_ROWS_PER_WG")) {
+        int v = atoi(e);
+        if (v >= kGemvWaves && v % kGemvWaves == 0) return v;
+    }
     // Aim for >= 4 workgroups per CU on 256 CUs and one row per wave for long rows.
     int rpw = kGemvWaves;
     while ((long long)M / (rpw * 2) >= 1024 && nv * 16 * rpw * 2 <= 256 * 1024) rpw *= 2;
@@ -107,12 +204,46 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
     hipStream_t s = (hipStream_t)stream;
     const uint4 *A4 = reinterpret_cast<const uint4 *>(A);
     const uint4 *x4 = reinterpret_cast<const uint4 *>(x);
-    if (nv >= kWave * 16) {
-        hipLaunchKernelGGL((gemv_kernel<F16, 16>), dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
-                           nchunks, mode, rot);
-    } else {
-        hipLaunchKernelGGL((gemv_kernel<F16, 8>), dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
-                           nchunks, mode, rot);
+    bool done = false;
+    if (nv % kWave == 0) {
+        // smallest split S (1, 2, 4) with at most 8 vectors per lane per wave
+        const int C = nv / kWave;
+        int S = 1;
+        while (S < kGemvWaves && (C % (S * 2) == 0) && C / S > 8) S *= 2;
+        const int CW = C / S;
+        done = true;
+#define XD_GEMV_EXACT(CC, SS, DBB)                                                                        \
+    if (CW == CC && S == SS) {                                                                          \
+        hipLaunchKernelGGL((gemv_exact_kernel<F16, CC, SS, DBB>), dim3(grid), dim3(kGemvThreads), lds, s, A4, \
+                           x4, y, M, rpw, nchunks, mode, rot);                                          \
+    } else
+        XD_GEMV_EXACT(1, 1, true)
+        XD_GEMV_EXACT(2, 1, true)
+        XD_GEMV_EXACT(3, 1, true)
+        XD_GEMV_EXACT(4, 1, true)
+        XD_GEMV_EXACT(5, 1, true)
+        XD_GEMV_EXACT(6, 1, true)
+        XD_GEMV_EXACT(7, 1, true)
+        XD_GEMV_EXACT(8, 1, true)
+        XD_GEMV_EXACT(5, 2, true)
+        XD_GEMV_EXACT(6, 2, true)
+        XD_GEMV_EXACT(7, 2, true)
+        XD_GEMV_EXACT(8, 2, true)
+        XD_GEMV_EXACT(5, 4, true)
+        XD_GEMV_EXACT(6, 4, true)
+        XD_GEMV_EXACT(7, 4, true)
+        XD_GEMV_EXACT(8, 4, true)
+        { done = false; }
+#undef XD_GEMV_EXACT
+    }
+    if (!done) {
+        if (nv >= kWave * 16) {
+            hipLaunchKernelGGL((gemv_kernel<F16, 16>), dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
+                               nchunks, mode, rot);
+        } else {
+            hipLaunchKernelGGL((gemv_kernel<F16, 8>), dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
+                               nchunks, mode, rot);
+        }
     }
     return launch_status("gemv_kernel");
 }

@@ -42,6 +42,7 @@ class GemvF32:
     name = "gemv_f32_4096x4096"
     unit = "GB/s"
     dtype = "f32"
+    dominant = "gemv_f32"
 
     def __init__(self, M=4096, K=4096):
         import numpy as np
@@ -99,6 +100,7 @@ class GemvF32:
 class GemvF16(GemvF32):
     """fp16 W (N(0,0.02), seed 4243), x (N(0,1), seed 4244), fp32 accumulate."""
     dtype = "f16->f32"
+    dominant = "gemv_f16f32"
 
     def __init__(self, M=14336, K=4096):
         import numpy as np
@@ -146,12 +148,83 @@ class GemvF16(GemvF32):
                 "sample": f"{reps} full {self.M}x{self.K} fp16 GEMVs (oracle row loop)"}
 
 
+class Hist:
+    """2^28 u32 keys ~ Zipf(1.1) over 2^20 bins (seed 1373), bit-exact counts."""
+    name = "hist_2p28_zipf1.1_2p20bins"
+    unit = "Gkeys/s"
+    dtype = "u32"
+    dominant = "hist_partition"
+
+    def __init__(self, n=1 << 28, num_bins=1 << 20):
+        import torch
+        from l2domain_amd import gen
+        from l2domain_amd.histogram import HIST_SEED, ZIPF_S, Histogram
+        self.n, self.num_bins = n, num_bins
+        self.keys = gen.zipf_keys_device(n, num_bins, HIST_SEED, ZIPF_S)
+        self.h = Histogram(n, num_bins)
+        self.counts = torch.empty(num_bins, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        # SURVEY 8(d): 4 B per key read + 4 B per counter written
+        self.bytes = 4 * n + 4 * num_bins
+
+    def step(self, mode):
+        self.h(self.keys, self.counts, mode=mode)
+
+    def throughput(self, sec_per_step):
+        return self.n / sec_per_step / 1e9
+
+    def verify(self):
+        import numpy as np
+        import oracle as ora
+        host = self.keys.cpu().numpy().view(np.uint32)
+        ref, _ = ora.histogram(host, self.num_bins, nthreads=_cpu_threads())
+        self._host = host
+        ok = True
+        for mode in MODES:
+            self.step(mode)
+            got = self.counts.cpu().numpy().view(np.uint32)
+            ok = ok and bool(np.array_equal(got, ref))
+        return ok
+
+    def roofline(self, sec_per_launch):
+        # dominant kernel: the partition pass; its algorithmic traffic is the 4 B/key read
+        achieved = 4 * self.n / sec_per_launch / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "hist_partition_kernel",
+                "algorithmic_bytes_per_launch": 4 * self.n}
+
+    def op_roofline(self, sec_per_step):
+        achieved = self.bytes / sec_per_step / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": self.bytes}
+
+    def config(self):
+        return {"workload": self.name, "keys": self.n, "bins": self.num_bins, "zipf_s": 1.1, "seed": 1373,
+                "bin_map": "scrambled rank ((r+1)*0x9E3779B1 mod 2^20)"}
+
+    def cpu_baseline(self):
+        import numpy as np
+        import oracle as ora
+        nt = _cpu_threads()
+        sample = self._host[: 1 << 26] if hasattr(self, "_host") else self.keys[: 1 << 26].cpu().numpy().view(np.uint32)
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 5.0:
+            ora.histogram(sample, self.num_bins, nthreads=nt)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(sample.size / dt / 1e9, 4), "unit": "Gkeys/s", "cores": nt, "kind": "port",
+                "sample": f"{reps} x 2^26 keys of the same Zipf stream (oracle counting loop, HIST.cu:279-288, "
+                          f"{nt} threads with private histograms)"}
+
+
 WORKLOADS = {
+    "hist": Hist,
     "gemv_f32": GemvF32,
     "gemv_f16_up": lambda: GemvF16(14336, 4096),
     "gemv_f16_down": lambda: GemvF16(4096, 14336),
 }
-DEFAULT_WORKLOAD = "gemv_f32"
+DEFAULT_WORKLOAD = "hist"
 
 
 # ---------------------------------------------------------------------------------------
@@ -187,6 +260,22 @@ def time_steps(wl, mode, steps, warmup, flusher=None):
     return total / steps
 
 
+def kernel_times(wl, mode, steps, flusher=None):
+    """Per-kernel average launch duration (s) from the library's HIP events, over `steps` steps."""
+    import torch
+    from l2domain_amd import _lib
+    torch.cuda.synchronize()
+    _lib.timing_enable(True)
+    for _ in range(steps):
+        if flusher is not None:
+            flusher.flush()
+        wl.step(mode)
+    torch.cuda.synchronize()
+    t = _lib.timing_read()
+    _lib.timing_enable(False)
+    return {k: (ms / 1e3 / max(n, 1), n) for k, (ms, n) in t.items()}
+
+
 def run_workload(name, steps, warmup, cold=False, with_cpu=True):
     import torch
     from l2domain_amd.domain import CacheFlusher
@@ -197,11 +286,13 @@ def run_workload(name, steps, warmup, cold=False, with_cpu=True):
     for mode in MODES:
         res[mode] = time_steps(wl, mode, steps, warmup, flusher)
     torch.cuda.synchronize()
+    kt = kernel_times(wl, "aware", steps, flusher)
     out = {
         "workload": wl,
         "verified": ok,
         "sec": res,
         "tput": {m: wl.throughput(s) for m, s in res.items()},
+        "kernels": kt,
     }
     if with_cpu:
         out["cpu"] = wl.cpu_baseline()
@@ -253,10 +344,13 @@ def main():
                   for m in MODES},
         "speedup_aware_vs_oblivious": round(r["sec"]["oblivious"] / r["sec"]["aware"], 4),
         "speedup_rotated_vs_oblivious": round(r["sec"]["oblivious"] / r["sec"]["rotated"], 4),
-        "roofline": wl.roofline(sec),
+        "roofline": wl.roofline(r["kernels"][wl.dominant][0]),
+        "kernels_us": {k: round(v[0] * 1e6, 3) for k, v in r["kernels"].items()},
         "cpu_baseline": r.get("cpu"),
         "device": topology(0)["name"],
     }
+    if hasattr(wl, "op_roofline"):
+        line["roofline_op"] = wl.op_roofline(sec)
     if args.all:
         extras = {}
         for name in sorted(WORKLOADS):
@@ -268,7 +362,8 @@ def main():
                             "value_oblivious": round(e["tput"]["oblivious"], 3),
                             "value_rotated": round(e["tput"]["rotated"], 3),
                             "speedup_aware_vs_oblivious": round(e["sec"]["oblivious"] / e["sec"]["aware"], 4),
-                            "roofline": e["workload"].roofline(e["sec"]["aware"])}
+                            "roofline": e["workload"].roofline(e["kernels"][e["workload"].dominant][0]),
+                            "kernels_us": {k: round(v[0] * 1e6, 3) for k, v in e["kernels"].items()}}
         line["extras"] = extras
     print(json.dumps(line), flush=True)
 

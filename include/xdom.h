@@ -73,6 +73,15 @@ const char *xd_version(void);
 /* Message describing the last error raised on the calling thread ("" if none). */
 const char *xd_last_error(void);
 
+/* Per-kernel timing of the library's own launches, for benchmarks: when enabled, every
+ * kernel launch is bracketed by HIP events on its launch stream. xd_timing_enable resets
+ * the accumulators; xd_timing_query(i, ...) reports kernel number i (in first-launch order)
+ * with its summed duration and launch count, waiting for outstanding launches; it returns
+ * XD_ERR_INVALID_ARG past the last kernel. No counterpart in the reference (which times
+ * whole kernels with cudaEvent pairs in each main(), e.g. GEMV.cu:301-316). */
+int xd_timing_enable(int on);
+int xd_timing_query(int index, char *name, int name_len, double *total_ms, long long *launches);
+
 /* Static description of the device. Replaces the latency-probed SM->side map
  * latopt::get_map_smid2side (utility/latopt.cuh:487-562): on CDNA the L2 domain of a
  * workgroup is read from the hardware (HW_REG_XCC_ID), so nothing has to be probed. */
@@ -111,6 +120,23 @@ int xd_gemv_f16f32(const uint16_t *W, const uint16_t *x, float *y, int M, int K,
                    void *stream);
 
 /* ------------------------------------------------------------------------------------ */
+/* Histogram  counts[k] = #{i : keys[i] == k}, k < num_bins                               */
+/* ------------------------------------------------------------------------------------ */
+
+/* Workspace bytes xd_hist_u32 needs for n keys and num_bins counters (0 if num_bins is out
+ * of range). About 2 bytes per key plus 128 KB per counting workgroup. */
+size_t xd_hist_workspace_size(size_t n, uint32_t num_bins);
+
+/* Histogram of uint32 keys into num_bins (1..2^24) uint32 counters; keys >= num_bins are
+ * not counted. Every counts[k] is written (no accumulation into counts). n < 2^32.
+ * Replaces histogram256_chunked_kernel / histogram256_persistent_kernel /
+ * merge_histogram256_kernel (applications/histogram/src/histogram256_sideaware.cu:51-157),
+ * generalised from 256 byte-bins (add_word, :20-25) to one bin per key. XD_MODE_AWARE
+ * range-partitions the bins over the XCDs: XCD x counts and merges only its bin range. */
+int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int mode,
+                void *workspace, size_t workspace_bytes, void *stream);
+
+/* ------------------------------------------------------------------------------------ */
 /* Seeded input generators (host). Fully specified integer mixers; no libc RNG.          */
 /* ------------------------------------------------------------------------------------ */
 
@@ -122,6 +148,17 @@ int xd_gen_uniform_f32(float *out, size_t n, uint64_t seed);
 
 /* out[i] = binary16(RNE) of mean + stddev * N(0,1), Box-Muller over xd_rand64(seed, .). */
 int xd_gen_normal_f16(uint16_t *out, size_t n, double mean, double stddev, uint64_t seed);
+
+/* Zipf(s) over num_bins ranks as 64-bit inverse-CDF thresholds (host, fp64):
+ * out[k] = floor(2^64 * sum_{r<=k} (r+1)^-s / H), out[num_bins-1] = 2^64-1. */
+int xd_zipf_thresholds(uint64_t *out, uint32_t num_bins, double s);
+
+/* Device generator: keys[i] = scramble(least k with xd_rand64(seed, i) < thresholds[k]),
+ * thresholds a device copy of xd_zipf_thresholds. With scramble != 0 and num_bins a power
+ * of two, rank r maps to bin ((r + 1) * 0x9E3779B1) mod num_bins (a bijection), so hot
+ * ranks are spread over the bin range; otherwise bin = rank. Enqueued on `stream`. */
+int xd_gen_zipf_keys(uint32_t *keys, size_t n, const uint64_t *thresholds, uint32_t num_bins,
+                     uint64_t seed, int scramble, void *stream);
 
 #ifdef __cplusplus
 }

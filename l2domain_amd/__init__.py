@@ -2,8 +2,16 @@
 
 Python host mirror of the C ABI in include/xdom.h. Device buffers are torch tensors on a
 ROCm device (torch is used only for device memory and streams); every compute call goes
-to libxdom.so, and importing this package fails if that library is not built.
+to libxdom.so. The library is loaded by the first module that needs it (l2domain_amd._lib)
+and that import fails if the library is not built: there is no CPU fallback.
 """
-from ._lib import (MODE_AWARE, MODE_OBLIVIOUS, MODE_ROTATED, MODES, XdomError, lib)  # noqa: F401
+MODE_OBLIVIOUS = 0
+MODE_AWARE = 1
+MODE_ROTATED = 2
 
-__all__ = ["MODE_AWARE", "MODE_OBLIVIOUS", "MODE_ROTATED", "MODES", "XdomError", "lib"]
+
+def __getattr__(name):
+    if name in ("lib", "XdomError", "MODES"):
+        from . import _lib
+        return getattr(_lib, name)
+    raise AttributeError(name)

@@ -56,15 +56,21 @@ D = C.c_double
 SIGNATURES: dict[str, tuple] = {
     "xd_version": (C.c_char_p, []),
     "xd_last_error": (C.c_char_p, []),
+    "xd_timing_enable": (I, [I]),
+    "xd_timing_query": (I, [I, C.c_char_p, I, C.POINTER(D), C.POINTER(C.c_longlong)]),
     "xd_topology_query": (I, [I, C.POINTER(Topology)]),
     "xd_domain_scan": (I, [I, VP, VP]),
     "xd_cache_flush_bytes": (SZ, []),
     "xd_cache_flush": (I, [VP, SZ, VP]),
     "xd_gemv_f32": (I, [VP, VP, VP, I, I, I, VP]),
     "xd_gemv_f16f32": (I, [VP, VP, VP, I, I, I, VP]),
+    "xd_hist_workspace_size": (SZ, [SZ, U32]),
+    "xd_hist_u32": (I, [VP, SZ, VP, U32, I, VP, SZ, VP]),
     "xd_rand64": (U64, [U64, U64]),
     "xd_gen_uniform_f32": (I, [VP, SZ, U64]),
     "xd_gen_normal_f16": (I, [VP, SZ, D, D, U64]),
+    "xd_zipf_thresholds": (I, [VP, U32, D]),
+    "xd_gen_zipf_keys": (I, [VP, SZ, VP, U32, U64, I, VP]),
 }
 
 
@@ -94,3 +100,22 @@ def call(name: str, *args):
     rc = getattr(lib, name)(*args)
     check(rc, name)
     return rc
+
+
+def timing_enable(on: bool = True) -> None:
+    call("xd_timing_enable", 1 if on else 0)
+
+
+def timing_read() -> dict:
+    """{kernel name: (total_ms, launches)} for the library's launches since timing_enable()."""
+    out = {}
+    i = 0
+    buf = C.create_string_buffer(128)
+    while True:
+        ms = C.c_double()
+        n = C.c_longlong()
+        if lib.xd_timing_query(i, buf, 128, C.byref(ms), C.byref(n)) != XD_OK:
+            break
+        out[buf.value.decode()] = (ms.value, n.value)
+        i += 1
+    return out

@@ -42,6 +42,30 @@ inline int launch_status(const char *what) {
     return XD_OK;
 }
 
+// Opt-in per-kernel timing (xd_timing_enable): HIP events around the library's own launches,
+// recorded on the launch stream. No cost when disabled.
+bool timing_enabled();
+void timing_record(const char *kernel, hipEvent_t start, hipEvent_t stop);
+
+class KernelTimer {
+  public:
+    KernelTimer(const char *kernel, hipStream_t s) : name_(kernel), s_(s) {
+        if (timing_enabled() && hipEventCreate(&e0_) == hipSuccess && hipEventCreate(&e1_) == hipSuccess)
+            on_ = hipEventRecord(e0_, s_) == hipSuccess;
+    }
+    ~KernelTimer() {
+        if (on_ && hipEventRecord(e1_, s_) == hipSuccess) timing_record(name_, e0_, e1_);
+    }
+    KernelTimer(const KernelTimer &) = delete;
+    KernelTimer &operator=(const KernelTimer &) = delete;
+
+  private:
+    const char *name_;
+    hipStream_t s_;
+    hipEvent_t e0_ = nullptr, e1_ = nullptr;
+    bool on_ = false;
+};
+
 // Per-device pass counter used by XD_MODE_ROTATED (advances once per pass).
 unsigned next_rotation(int passes);
 

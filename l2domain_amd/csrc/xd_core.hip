@@ -6,6 +6,8 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "xd_common.hpp"
 
@@ -33,6 +35,44 @@ unsigned next_rotation(int passes) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     return g_rotation[dev].fetch_add((unsigned)passes) + 1u;
+}
+
+// ---- opt-in kernel timing ----
+struct TimingRec {
+    std::string name;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> pending;
+    double total_ms = 0.0;
+    long long launches = 0;
+};
+static std::mutex g_tmu;
+static std::atomic<bool> g_timing{false};
+static std::vector<TimingRec> g_recs;
+
+bool timing_enabled() { return g_timing.load(std::memory_order_relaxed); }
+
+void timing_record(const char *kernel, hipEvent_t start, hipEvent_t stop) {
+    std::lock_guard<std::mutex> lk(g_tmu);
+    for (auto &r : g_recs)
+        if (r.name == kernel) {
+            r.pending.emplace_back(start, stop);
+            return;
+        }
+    g_recs.push_back(TimingRec{kernel, {{start, stop}}, 0.0, 0});
+}
+
+static void timing_drain_locked() {
+    for (auto &r : g_recs) {
+        for (auto &p : r.pending) {
+            float ms = 0.0f;
+            if (hipEventSynchronize(p.second) == hipSuccess && hipEventElapsedTime(&ms, p.first, p.second) == hipSuccess) {
+                r.total_ms += ms;
+                r.launches += 1;
+            }
+            (void)hipEventDestroy(p.first);
+            (void)hipEventDestroy(p.second);
+        }
+        r.pending.clear();
+    }
 }
 
 // DomainScan: every workgroup records where the hardware placed it.
@@ -68,6 +108,25 @@ extern "C" {
 const char *xd_version(void) { return "xdom 0.1.0 (gfx950)"; }
 
 const char *xd_last_error(void) { return g_last_error.c_str(); }
+
+int xd_timing_enable(int on) {
+    std::lock_guard<std::mutex> lk(g_tmu);
+    timing_drain_locked();
+    g_recs.clear();
+    g_timing.store(on != 0);
+    return XD_OK;
+}
+
+int xd_timing_query(int index, char *name, int name_len, double *total_ms, long long *launches) {
+    std::lock_guard<std::mutex> lk(g_tmu);
+    timing_drain_locked();
+    if (index < 0 || index >= (int)g_recs.size()) return XD_ERR_INVALID_ARG;
+    const TimingRec &r = g_recs[(size_t)index];
+    if (name && name_len > 0) std::snprintf(name, (size_t)name_len, "%s", r.name.c_str());
+    if (total_ms) *total_ms = r.total_ms;
+    if (launches) *launches = r.launches;
+    return XD_OK;
+}
 
 int xd_topology_query(int device, xd_topology_t *out) {
     XD_REQUIRE(out != nullptr, "xd_topology_query: out is NULL");

@@ -204,6 +204,7 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
     hipStream_t s = (hipStream_t)stream;
     const uint4 *A4 = reinterpret_cast<const uint4 *>(A);
     const uint4 *x4 = reinterpret_cast<const uint4 *>(x);
+    KernelTimer kt(F16 ? "gemv_f16f32" : "gemv_f32", s);
     bool done = false;
     if (nv % kWave == 0) {
         // smallest split S (1, 2, 4) with at most 8 vectors per lane per wave

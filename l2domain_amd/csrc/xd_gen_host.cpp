@@ -114,4 +114,18 @@ int xd_gen_normal_f16(uint16_t *out, size_t n, double mean, double stddev, uint6
     return XD_OK;
 }
 
+int xd_zipf_thresholds(uint64_t *out, uint32_t num_bins, double s) {
+    if (out == nullptr || num_bins == 0 || !(s > 0.0)) return XD_ERR_INVALID_ARG;
+    // P(rank = k) = (k+1)^-s / H, H = sum_{r=1..N} r^-s accumulated in rank order.
+    double H = 0.0;
+    for (uint32_t r = 1; r <= num_bins; ++r) H += pow((double)r, -s);
+    double cum = 0.0;
+    for (uint32_t k = 0; k < num_bins; ++k) {
+        cum += pow((double)(k + 1), -s);
+        const double f = cum / H;
+        out[k] = (k + 1 == num_bins || f >= 1.0) ? UINT64_MAX : (uint64_t)ldexp(f, 64);
+    }
+    return XD_OK;
+}
+
 }  // extern "C"

@@ -27,6 +27,24 @@ def normal_f16(n: int, mean: float, stddev: float, seed: int) -> np.ndarray:
     return out.view(np.float16)
 
 
+def zipf_thresholds(num_bins: int, s: float = 1.1) -> np.ndarray:
+    out = np.empty(num_bins, dtype=np.uint64)
+    _lib.call("xd_zipf_thresholds", out.ctypes.data, num_bins, s)
+    return out
+
+
+def zipf_keys_device(n: int, num_bins: int, seed: int, s: float = 1.1, scramble: bool = True,
+                     thresholds=None, out=None):
+    """Draws n Zipf(s) keys on the current device (torch int32 tensor holding u32 keys)."""
+    import torch
+    from ._torch import stream_handle
+    t = thresholds if thresholds is not None else torch.from_numpy(zipf_thresholds(num_bins, s).view(np.int64)).cuda()
+    keys = out if out is not None else torch.empty(n, dtype=torch.int32, device="cuda")
+    _lib.call("xd_gen_zipf_keys", keys.data_ptr() if n else None, n, t.data_ptr(), num_bins, seed,
+              1 if scramble else 0, stream_handle())
+    return keys
+
+
 def gemv_f32_inputs(M: int, K: int, seed: int = SEED_GEMV_F32):
     """A[M,K], x[K]: U[-1,1) on a 2^-23 grid (configs[0] of the build)."""
     return uniform_f32(M * K, seed).reshape(M, K), uniform_f32(K, seed + X_SEED_OFFSET)

@@ -35,6 +35,11 @@ _SIGS = {
     "ora_gemv_f32_seq": (None, [VP, VP, VP, I64, I64, I]),
     "ora_gemv_f32_f64": (None, [VP, VP, VP, VP, I64, I64, I]),
     "ora_gemv_f16_f64": (None, [VP, VP, VP, VP, I64, I64, I]),
+    "ora_zipf_thresholds": (None, [VP, U32, D]),
+    "ora_gen_zipf_keys": (None, [VP, SZ, VP, U32, U64, I]),
+    "ora_zipf_key_at": (U32, [VP, U32, U64, I, U64]),
+    "ora_zipf_scramble": (U32, [U32, U32]),
+    "ora_histogram": (U64, [VP, SZ, VP, U32, I]),
 }
 for _n, (_r, _a) in _SIGS.items():
     _f = getattr(lib, _n)
@@ -97,3 +102,31 @@ def gemv_f64(A: np.ndarray, x: np.ndarray, nthreads: int = 1):
     else:
         raise TypeError(A.dtype)
     return y, yabs
+
+
+def zipf_thresholds(num_bins: int, s: float) -> np.ndarray:
+    t = np.empty(num_bins, dtype=np.uint64)
+    lib.ora_zipf_thresholds(_p(t), num_bins, s)
+    return t
+
+
+def zipf_keys(n: int, t: np.ndarray, seed: int, scramble: bool = True) -> np.ndarray:
+    keys = np.empty(n, dtype=np.uint32)
+    lib.ora_gen_zipf_keys(_p(keys), n, _p(t), len(t), seed, 1 if scramble else 0)
+    return keys
+
+
+def zipf_key_at(t: np.ndarray, seed: int, index: int, scramble: bool = True) -> int:
+    return int(lib.ora_zipf_key_at(_p(t), len(t), seed, 1 if scramble else 0, index))
+
+
+def zipf_scramble(rank: int, num_bins: int) -> int:
+    return int(lib.ora_zipf_scramble(rank, num_bins))
+
+
+def histogram(keys: np.ndarray, num_bins: int, nthreads: int = 1) -> tuple[np.ndarray, int]:
+    """HIST.cu:279-288 generalised: returns (counts u32[num_bins], number of keys counted)."""
+    keys = np.ascontiguousarray(keys).view(np.uint32)
+    counts = np.empty(num_bins, dtype=np.uint32)
+    c = lib.ora_histogram(_p(keys), keys.size, _p(counts), num_bins, nthreads)
+    return counts, int(c)

@@ -206,3 +206,90 @@ void ora_gemv_f16_f64(const uint16_t *W, const uint16_t *x, double *y, double *y
     gemv_ctx c = {W, x, NULL, y, yabs, K};
     parallel_range(M, nthreads, gemv_f16_rows, &c);
 }
+
+/* ------------------------------------------------------------------------------------ */
+/* histogram                                                                             */
+/* ------------------------------------------------------------------------------------ */
+void ora_zipf_thresholds(uint64_t *t, uint32_t num_bins, double s) {
+    /* H = sum_{r=1..N} r^-s, accumulated in rank order in double. */
+    double H = 0.0;
+    for (uint32_t r = 1; r <= num_bins; ++r) H += pow((double)r, -s);
+    double cum = 0.0;
+    for (uint32_t k = 0; k < num_bins; ++k) {
+        cum += pow((double)(k + 1), -s);
+        double f = cum / H;
+        if (k + 1 == num_bins || f >= 1.0) t[k] = UINT64_MAX;
+        else t[k] = (uint64_t)ldexp(f, 64);
+    }
+}
+
+uint32_t ora_zipf_scramble(uint32_t rank, uint32_t num_bins) {
+    /* affine bijection on [0, 2^m): (rank + 1) * 0x9E3779B1 mod 2^m; identity otherwise */
+    if (num_bins == 0 || (num_bins & (num_bins - 1))) return rank;
+    return (uint32_t)(((uint64_t)(rank + 1) * 0x9E3779B1ULL) & (num_bins - 1));
+}
+
+uint32_t ora_zipf_key_at(const uint64_t *t, uint32_t num_bins, uint64_t seed, int scramble, uint64_t index) {
+    uint64_t u = ora_splitmix64(seed, index);
+    uint32_t k = 0;
+    while (k + 1 < num_bins && !(u < t[k])) ++k; /* linear search: independent of the device's bisection */
+    return scramble ? ora_zipf_scramble(k, num_bins) : k;
+}
+
+void ora_gen_zipf_keys(uint32_t *keys, size_t n, const uint64_t *t, uint32_t num_bins, uint64_t seed,
+                       int scramble) {
+    for (size_t i = 0; i < n; ++i) keys[i] = ora_zipf_key_at(t, num_bins, seed, scramble, i);
+}
+
+typedef struct {
+    const uint32_t *keys;
+    uint32_t num_bins;
+    uint32_t **priv;
+    uint64_t *counted;
+    int64_t per;
+} hist_ctx;
+
+static void hist_part(void *p, int64_t b, int64_t e) {
+    hist_ctx *c = (hist_ctx *)p;
+    int64_t t = b / c->per;
+    uint32_t *h = c->priv[t];
+    uint64_t cnt = 0;
+    for (int64_t i = b; i < e; ++i) {
+        uint32_t k = c->keys[i];
+        if (k < c->num_bins) {
+            h[k]++;
+            cnt++;
+        }
+    }
+    c->counted[t] = cnt;
+}
+
+/* HIST.cu:279-288: serial counting loop; with nthreads > 1, private histograms then a sum. */
+uint64_t ora_histogram(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int nthreads) {
+    memset(counts, 0, sizeof(uint32_t) * num_bins);
+    if (nthreads <= 1 || n < 4096) {
+        uint64_t cnt = 0;
+        for (size_t i = 0; i < n; ++i)
+            if (keys[i] < num_bins) {
+                counts[keys[i]]++;
+                cnt++;
+            }
+        return cnt;
+    }
+    if (nthreads > 256) nthreads = 256;
+    uint32_t *priv[256];
+    uint64_t counted[256];
+    for (int t = 0; t < nthreads; ++t) {
+        priv[t] = (uint32_t *)calloc(num_bins, sizeof(uint32_t));
+        counted[t] = 0;
+    }
+    hist_ctx c = {keys, num_bins, priv, counted, (int64_t)((n + nthreads - 1) / nthreads)};
+    parallel_range((int64_t)n, nthreads, hist_part, &c);
+    uint64_t total = 0;
+    for (int t = 0; t < nthreads; ++t) {
+        for (uint32_t k = 0; k < num_bins; ++k) counts[k] += priv[t][k];
+        total += counted[t];
+        free(priv[t]);
+    }
+    return total;
+}

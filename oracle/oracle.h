@@ -30,4 +30,16 @@ void ora_gemv_f32_f64(const float *A, const float *x, double *y, double *yabs, i
 void ora_gemv_f16_f64(const uint16_t *W, const uint16_t *x, double *y, double *yabs, int64_t M,
                       int64_t K, int nthreads);
 
+
+/* ---- histogram (HIST.cu:279-299, generalised from 256 byte-bins to num_bins key bins) ---- */
+/* Zipf(s) over num_bins ranks: t[k] = floor(2^64 * P(rank <= k)), t[num_bins-1] = 2^64-1. */
+void ora_zipf_thresholds(uint64_t *t, uint32_t num_bins, double s);
+/* key i = scramble(rank(splitmix64(seed, i))) with rank = least k, u < t[k]. */
+void ora_gen_zipf_keys(uint32_t *keys, size_t n, const uint64_t *t, uint32_t num_bins, uint64_t seed,
+                       int scramble);
+uint32_t ora_zipf_scramble(uint32_t rank, uint32_t num_bins);
+uint32_t ora_zipf_key_at(const uint64_t *t, uint32_t num_bins, uint64_t seed, int scramble, uint64_t index);
+/* counts[k] = #{i : keys[i] == k}; keys >= num_bins are not counted. Returns the number counted. */
+uint64_t ora_histogram(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int nthreads);
+
 #endif

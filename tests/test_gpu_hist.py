@@ -1,0 +1,82 @@
+"""Histogram parity on the GPU: xd_hist_u32 (through the C ABI) against the oracle's
+counting loop (HIST.cu:279-288 generalised to one bin per key). Bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as ora
+from l2domain_amd import gen
+from l2domain_amd.histogram import HIST_BINS, HIST_KEYS, HIST_SEED, ZIPF_S, Histogram
+
+pytestmark = pytest.mark.gpu
+MODES = ["oblivious", "aware", "rotated"]
+
+
+def gpu_hist(keys_np: np.ndarray, num_bins: int, mode, h: Histogram | None = None):
+    keys = torch.from_numpy(keys_np.view(np.int32)).cuda()
+    h = h or Histogram(max(len(keys_np), 1), num_bins)
+    counts = torch.full((num_bins,), -7, dtype=torch.int32, device="cuda")
+    h(keys, counts, mode=mode)
+    torch.cuda.synchronize()
+    return counts.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("n,num_bins", [(0, 1000), (1, 1), (1000, 256), (32767, 32768), (32768, 32769),
+                                        (32769, 65536), (100000, 1 << 20), (300001, 1 << 24), (70000, 1000003)])
+def test_uniform_keys(n, num_bins, mode):
+    rng = np.random.default_rng(n + num_bins)
+    keys = rng.integers(0, int(num_bins * 1.1) + 1, size=n, dtype=np.int64).astype(np.uint32)  # some out of range
+    ref, _ = ora.histogram(keys, num_bins)
+    np.testing.assert_array_equal(gpu_hist(keys, num_bins, mode), ref)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_single_hot_bin_and_sorted_keys(mode):
+    n = (1 << 22) + 5
+    keys = np.full(n, 123457, dtype=np.uint32)
+    ref, _ = ora.histogram(keys, 1 << 20)
+    np.testing.assert_array_equal(gpu_hist(keys, 1 << 20, mode), ref)
+    keys = np.sort(np.random.default_rng(3).integers(0, 1 << 20, size=n).astype(np.uint32))
+    ref, _ = ora.histogram(keys, 1 << 20)
+    np.testing.assert_array_equal(gpu_hist(keys, 1 << 20, mode), ref)
+
+
+def test_workspace_reuse_shrinking_input():
+    h = Histogram(1 << 20, 1 << 20)
+    rng = np.random.default_rng(9)
+    for n in (1 << 20, 12345, 1 << 19):
+        keys = rng.integers(0, 1 << 20, size=n).astype(np.uint32)
+        ref, _ = ora.histogram(keys, 1 << 20)
+        for mode in MODES:
+            np.testing.assert_array_equal(gpu_hist(keys, 1 << 20, mode, h), ref)
+
+
+@pytest.fixture(scope="module")
+def config_keys():
+    keys = gen.zipf_keys_device(HIST_KEYS, HIST_BINS, HIST_SEED, ZIPF_S)
+    torch.cuda.synchronize()
+    host = keys.cpu().numpy().view(np.uint32)
+    ref, counted = ora.histogram(host, HIST_BINS, nthreads=16)
+    return keys, host, ref, counted
+
+
+def test_device_zipf_keys_match_oracle_generator(config_keys):
+    _, host, _, _ = config_keys
+    t = ora.zipf_thresholds(HIST_BINS, ZIPF_S)
+    idx = np.random.default_rng(1).integers(0, HIST_KEYS, size=300)
+    for i in list(idx) + [0, 1, HIST_KEYS - 1]:
+        assert host[i] == ora.zipf_key_at(t, HIST_SEED, int(i))
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_config_2p28_zipf(config_keys, mode):
+    keys, _, ref, counted = config_keys
+    assert counted == HIST_KEYS
+    h = Histogram(HIST_KEYS, HIST_BINS)
+    counts = torch.empty(HIST_BINS, dtype=torch.int32, device="cuda")
+    h(keys, counts, mode=mode)
+    torch.cuda.synchronize()
+    got = counts.cpu().numpy().view(np.uint32)
+    assert int(got.astype(np.uint64).sum()) == HIST_KEYS
+    np.testing.assert_array_equal(got, ref)

@@ -118,3 +118,66 @@ def test_gemv_f16_uses_half_values():
     y, _ = ora.gemv_f64(W, x)
     ref = W.astype(np.float64) @ x.astype(np.float64)
     np.testing.assert_allclose(y, ref, rtol=0, atol=1e-13)
+
+
+# ---------------------------------------------------------------------------------------
+# histogram and Zipf generator
+# ---------------------------------------------------------------------------------------
+def test_histogram_matches_numpy_bincount():
+    rng = np.random.default_rng(17)
+    keys = rng.integers(0, 1200, size=50000).astype(np.uint32)  # includes keys >= num_bins
+    for nt in (1, 4):
+        counts, counted = ora.histogram(keys, 1000, nthreads=nt)
+        ref = np.bincount(keys[keys < 1000], minlength=1000)
+        np.testing.assert_array_equal(counts, ref)
+        assert counted == int((keys < 1000).sum())
+
+
+def test_histogram_second_method_sort_runlength():
+    rng = np.random.default_rng(18)
+    keys = (rng.zipf(1.3, size=20000) % 4096).astype(np.uint32)
+    counts, _ = ora.histogram(keys, 4096)
+    u, c = np.unique(keys, return_counts=True)
+    ref = np.zeros(4096, dtype=np.int64)
+    ref[u] = c
+    np.testing.assert_array_equal(counts, ref)
+
+
+def test_zipf_thresholds_normalisation_matches_hurwitz_zeta():
+    from scipy.special import zeta
+    for N, s in ((1 << 20, 1.1), (1000, 1.1), (64, 2.0)):
+        t = ora.zipf_thresholds(N, s)
+        assert np.all(np.diff(t.astype(np.float64)) >= 0) and t[-1] == 2**64 - 1
+        H = zeta(s, 1) - zeta(s, N + 1)  # generalised harmonic number H_{N,s}
+        assert abs(t[0] / 2.0**64 - 1.0 / H) < 1e-9
+        k = N // 2  # P(rank <= k) = H_{k+1,s} / H_{N,s}
+        assert abs(t[k] / 2.0**64 - (zeta(s, 1) - zeta(s, k + 2)) / H) < 1e-9
+
+
+def test_zipf_top_bin_share_for_config():
+    t = ora.zipf_thresholds(1 << 20, 1.1)
+    assert abs(t[0] / 2.0**64 - 0.1237) < 5e-4  # 12.4% of keys in the hottest bin
+
+
+def test_zipf_keys_follow_the_pmf():
+    from scipy.stats import chisquare
+    N, s, n = 32, 1.1, 100000
+    t = ora.zipf_thresholds(N, s)
+    keys = ora.zipf_keys(n, t, seed=5, scramble=False)
+    obs = np.bincount(keys, minlength=N)
+    p = np.arange(1, N + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    assert chisquare(obs, p * n).pvalue > 1e-4
+
+
+def test_zipf_scramble_is_a_bijection():
+    N = 1 << 12
+    img = {ora.zipf_scramble(r, N) for r in range(N)}
+    assert img == set(range(N))
+    assert ora.zipf_scramble(5, 1000) == 5  # identity when num_bins is not a power of two
+
+
+def test_product_zipf_thresholds_match_oracle():
+    from l2domain_amd import gen
+    for N, s in ((1 << 20, 1.1), (777, 1.5), (1, 1.1)):
+        np.testing.assert_array_equal(gen.zipf_thresholds(N, s), ora.zipf_thresholds(N, s))

@@ -28,7 +28,7 @@ namespace xd {
 
 constexpr int kHB = 15;
 constexpr uint32_t kBucketBins = 1u << kHB;  // 32768 counters = 128 KB of LDS
-constexpr int kTileKeys = 32768;
+constexpr int kTileKeys = 16384;
 constexpr int kP1Threads = 1024;
 constexpr int kP1Vec = kTileKeys / 4 / kP1Threads;  // uint4 loads per thread (8)
 constexpr int kMaxBuckets = 512;                    // num_bins <= 2^24
@@ -137,28 +137,13 @@ hist_partition_kernel(const uint32_t *__restrict__ keys, size_t n, uint32_t num_
     }
     __syncthreads();
 
-    // Slot of every key inside its bucket. The wave's most common bucket is taken first
-    // with one LDS add for the whole group; the remaining lanes add one by one.
+    // Slot of every key inside its bucket: a returning LDS add per key. (Same-bucket lanes
+    // of a wave serialise in the LDS, which costs less than aggregating them in registers.)
     uint32_t pos[4 * kP1Vec];
 #pragma unroll
     for (int j = 0; j < 4 * kP1Vec; ++j) {
         const uint32_t key = kk[j];
-        const bool valid = key < num_bins;
-        const uint32_t b = key >> kHB;
-        uint32_t off = 0;
-        const uint64_t act = __ballot(valid);
-        if (act) {
-            const int first = __builtin_ctzll(act);
-            const uint32_t vb = (uint32_t)__builtin_amdgcn_readlane((int)b, first);
-            const bool same = valid && b == vb;
-            const uint64_t sm = __ballot(same);
-            uint32_t gb = 0;
-            if (lane == first) gb = atomicAdd(&cnt[vb], (uint32_t)__builtin_popcountll(sm));
-            gb = (uint32_t)__builtin_amdgcn_readlane((int)gb, first);
-            if (same) off = gb + mask_rank(sm);
-            else if (valid) off = atomicAdd(&cnt[b], 1u);
-        }
-        pos[j] = off;
+        pos[j] = key < num_bins ? atomicAdd(&cnt[key >> kHB], 1u) : 0u;
     }
     __syncthreads();
 
@@ -327,22 +312,31 @@ hist_plan_kernel(const uint32_t *__restrict__ tot, int nb, int ntiles, int per_x
 // ---------------------------------------------------------------------------------------
 // 3. count
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ void lds_count(uint32_t *h, uint32_t k, bool valid) {
-    const uint64_t act = __ballot(valid);
-    if (!act) return;
-    const int first = __builtin_ctzll(act);
-    const uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)k, first);
-    const bool same = valid && k == v;
-    const uint64_t sm = __ballot(same);
-    if (lane_id() == first) atomicAdd(&h[v], (uint32_t)__builtin_popcountll(sm));
-    if (valid && !same) atomicAdd(&h[k], 1u);
+constexpr uint32_t kTrash = kBucketBins;  // LDS slot that absorbs elements outside a run
+
+// Counts the 8 u16 keys of one 16-byte vector whose first element has index `e`, for the
+// run [s0, e0). Keys equal to the wave's current hot key go to the per-lane register
+// counter `hc` (the hot key of a Zipf bucket would otherwise make most lanes of a wave
+// hit one LDS address); all others take one ds_add each.
+__device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t e, uint32_t s0, uint32_t e0,
+                                          uint32_t hot, uint32_t &hc) {
+    if (e >= e0 || e + 8 <= s0) return;  // vector outside the run (most lanes' 2nd vector)
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t len = e0 - s0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        uint32_t key = (k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu);
+        key = (e + (uint32_t)k - s0 < len) ? key : kTrash;
+        if (key == hot) ++hc;
+        else atomicAdd(&h[key], 1u);
+    }
 }
 
 __global__ void __launch_bounds__(kP2Threads)
 hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb,
                   const HistItem *__restrict__ items, int per_xcd, uint32_t *__restrict__ partials, int mode,
                   unsigned rot) {
-    __shared__ __attribute__((aligned(16))) uint32_t h[kBucketBins];
+    __shared__ __attribute__((aligned(16))) uint32_t h[kBucketBins + 4];
     const int g = (int)blockIdx.x;
     int item;
     if (mode == XD_MODE_OBLIVIOUS) {
@@ -355,12 +349,22 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     if (it.bucket < 0) return;
     const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     uint4 *h4 = reinterpret_cast<uint4 *>(h);
-    for (int i = tid; i < (int)(kBucketBins / 4); i += kP2Threads) h4[i] = make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < (int)(kBucketBins / 4) + 1; i += kP2Threads) h4[i] = make_uint4(0, 0, 0, 0);
     __syncthreads();
 
     const int b = it.bucket;
+    uint32_t hot = kTrash + 1;  // no hot key yet
+    uint32_t hc = 0;
+    auto flush_hot = [&]() {
+        const uint32_t tot_hot = wave_sum_u32(hc);
+        if (lane == 0 && tot_hot) atomicAdd(&h[hot], tot_hot);
+        hc = 0;
+    };
+    // Each wave walks the tiles t0 + wave, t0 + wave + 16, ...: lane i first fetches the run
+    // bounds of 64 of them, then the wave counts run after run. A run is read as 16-byte
+    // vectors (8 keys); the first two vectors per lane of the next run are loaded before
+    // the current run is counted.
     for (int tb = it.t0 + wave; tb < it.t1; tb += kP2Waves * kWave) {
-        // lane i fetches the run bounds of tile tb + i * waves
         const int tl = tb + lane * kP2Waves;
         uint32_t rs = 0, re = 0;
         if (tl < it.t1) {
@@ -369,18 +373,54 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
             re = o[1];
         }
         const int ntl = min(kWave, (it.t1 - tb + kP2Waves - 1) / kP2Waves);
+        auto load2 = [&](int i, uint4 &v0, uint4 &v1) {
+            const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
+            const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
+            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
+            const uint32_t v = (s0 >> 3) + (uint32_t)lane, vend = (e0 + 7) >> 3;
+            v0 = v < vend ? run[v] : make_uint4(0, 0, 0, 0);
+            v1 = v + kWave < vend ? run[v + kWave] : make_uint4(0, 0, 0, 0);
+        };
+        uint4 c0, c1;
+        if (ntl > 0) load2(0, c0, c1);
         for (int i = 0; i < ntl; ++i) {
-            const uint32_t s = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
-            const uint32_t e = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
-            const uint32_t *run = reinterpret_cast<const uint32_t *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
-            const uint32_t wend = (e + 1) >> 1;
-            for (uint32_t w = (s >> 1) + (uint32_t)lane; w < wend; w += kWave) {
-                const uint32_t two = run[w];
-                lds_count(h, two & 0xffffu, 2 * w >= s);
-                lds_count(h, two >> 16, 2 * w + 1 < e);
+            uint4 n0 = make_uint4(0, 0, 0, 0), n1 = make_uint4(0, 0, 0, 0);
+            if (i + 1 < ntl) load2(i + 1, n0, n1);
+            const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
+            const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
+            const uint32_t v = (s0 >> 3) + (uint32_t)lane;
+            // Hot-key vote on the first key of every lane's first vector: keep the current
+            // hot key while a quarter of the samples match it, else adopt the first
+            // sample if a quarter of the samples match that one.
+            const uint32_t e8 = 8 * v;
+            const bool sv = e8 - s0 < e0 - s0;
+            const uint32_t sk = c0.x & 0xffffu;
+            if (__builtin_popcountll(__ballot(sv && sk == hot)) < kWave / 4) {
+                const uint64_t svm = __ballot(sv);
+                if (svm) {
+                    const uint32_t cand = (uint32_t)__builtin_amdgcn_readlane((int)sk, __builtin_ctzll(svm));
+                    if (__builtin_popcountll(__ballot(sv && sk == cand)) >= kWave / 4) {
+                        flush_hot();
+                        hot = cand;
+                    }
+                }
             }
+            count_vec(h, c0, e8, s0, e0, hot, hc);
+            count_vec(h, c1, 8 * (v + kWave), s0, e0, hot, hc);
+            // long runs (the hot bucket): remaining vectors, two per lane per trip
+            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
+            const uint32_t vend = (e0 + 7) >> 3;
+            for (uint32_t u = v + 2 * kWave; u < vend; u += 2 * kWave) {
+                const uint4 a0 = run[u];
+                const uint4 a1 = u + kWave < vend ? run[u + kWave] : make_uint4(0, 0, 0, 0);
+                count_vec(h, a0, 8 * u, s0, e0, hot, hc);
+                count_vec(h, a1, 8 * (u + kWave), s0, e0, hot, hc);
+            }
+            c0 = n0;
+            c1 = n1;
         }
     }
+    if (hot < kTrash) flush_hot();
     __syncthreads();
     uint4 *dst = reinterpret_cast<uint4 *>(partials + (size_t)item * kBucketBins);
     for (int i = tid; i < (int)(kBucketBins / 4); i += kP2Threads) dst[i] = h4[i];

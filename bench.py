@@ -218,8 +218,79 @@ class Hist:
                           f"{nt} threads with private histograms)"}
 
 
+class Hash:
+    """2^26 distinct u64 keys + values inserted at load factor 0.5 (2^27 slots),
+    then 2^26 lookups at 50% hits. A step = clear + insert + lookup."""
+    name = "hash_2p26_lf0.5_u64"
+    unit = "Mops/s"
+    dtype = "u64"
+    dominant = "hash_lookup"
+
+    def __init__(self):
+        import torch
+        from l2domain_amd.hashtable import HASH_KEYS, HASH_SEED, HASH_QSEED, HASH_SLOTS, HashTable, gen_kv, gen_queries
+        self.n, self.slots = HASH_KEYS, HASH_SLOTS
+        self.keys, self.vals = gen_kv(self.n, HASH_SEED)
+        self.q = gen_queries(self.n, self.n, HASH_SEED, HASH_QSEED)
+        self.t = HashTable(self.slots)
+        self.v = torch.empty(self.n, dtype=torch.int64, device="cuda")
+        self.f = torch.empty(self.n, dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+
+    def step(self, mode):
+        self.t.clear()
+        self.t.insert(self.keys, self.vals, mode=mode)
+        self.t.lookup(self.q, mode=mode, vals_out=self.v, found_out=self.f)
+
+    def throughput(self, sec_per_step):
+        return 2 * self.n / sec_per_step / 1e6
+
+    def verify(self):
+        import numpy as np
+        import oracle as ora
+        hk = self.keys.cpu().numpy().view(np.uint64)
+        hv = self.vals.cpu().numpy().view(np.uint64)
+        hq = self.q.cpu().numpy().view(np.uint64)
+        ref = ora.HashTable(self.slots)
+        ref.build(hk, hv)
+        rv, rf = ref.lookup(hq, nthreads=_cpu_threads())
+        self._ref = (hk, hv, hq)
+        ok = True
+        for mode in MODES:
+            self.step(mode)
+            ok = ok and self.t.failures() == 0
+            ok = ok and bool(np.array_equal(self.f.cpu().numpy(), rf))
+            ok = ok and bool(np.array_equal(self.v.cpu().numpy().view(np.uint64), rv))
+        return ok
+
+    def roofline(self, sec_per_launch):
+        # SURVEY 8(d): lookup = 8 B key + 16 B slot + 8 B value + 1 B found per query
+        achieved = 33 * self.n / sec_per_launch / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "hash_lookup_kernel",
+                "algorithmic_bytes_per_launch": 33 * self.n}
+
+    def config(self):
+        return {"workload": self.name, "keys": self.n, "slots": self.slots, "lookups": self.n, "hit_rate": 0.5,
+                "seed": 42}
+
+    def cpu_baseline(self):
+        import numpy as np
+        import oracle as ora
+        hk, hv, hq = self._ref
+        m = 1 << 23
+        t0 = time.perf_counter()
+        ref = ora.HashTable(1 << 24)
+        ref.build(hk[:m], hv[:m])
+        ref.lookup(hq[:m], nthreads=1)
+        dt = time.perf_counter() - t0
+        return {"value": round(2 * m / dt / 1e6, 3), "unit": "Mops/s", "cores": 1, "kind": "port",
+                "sample": "2^23 serial inserts into 2^24 slots + 2^23 lookups (oracle, HASH.cu:46-64,226-241)"}
+
+
 WORKLOADS = {
     "hist": Hist,
+    "hash": Hash,
     "gemv_f32": GemvF32,
     "gemv_f16_up": lambda: GemvF16(14336, 4096),
     "gemv_f16_down": lambda: GemvF16(4096, 14336),
@@ -287,12 +358,14 @@ def run_workload(name, steps, warmup, cold=False, with_cpu=True):
         res[mode] = time_steps(wl, mode, steps, warmup, flusher)
     torch.cuda.synchronize()
     kt = kernel_times(wl, "aware", steps, flusher)
+    kt_modes = {m: (kt if m == "aware" else kernel_times(wl, m, min(steps, 5), flusher)) for m in MODES}
     out = {
         "workload": wl,
         "verified": ok,
         "sec": res,
         "tput": {m: wl.throughput(s) for m, s in res.items()},
         "kernels": kt,
+        "kernels_by_mode": kt_modes,
     }
     if with_cpu:
         out["cpu"] = wl.cpu_baseline()
@@ -346,6 +419,8 @@ def main():
         "speedup_rotated_vs_oblivious": round(r["sec"]["oblivious"] / r["sec"]["rotated"], 4),
         "roofline": wl.roofline(r["kernels"][wl.dominant][0]),
         "kernels_us": {k: round(v[0] * 1e6, 3) for k, v in r["kernels"].items()},
+        "kernels_us_by_mode": {m: {k: round(v[0] * 1e6, 3) for k, v in kk.items()}
+                               for m, kk in r["kernels_by_mode"].items()},
         "cpu_baseline": r.get("cpu"),
         "device": topology(0)["name"],
     }

@@ -60,12 +60,23 @@ SIGNATURES: dict[str, tuple] = {
     "xd_timing_query": (I, [I, C.c_char_p, I, C.POINTER(D), C.POINTER(C.c_longlong)]),
     "xd_topology_query": (I, [I, C.POINTER(Topology)]),
     "xd_domain_scan": (I, [I, VP, VP]),
+    "xd_home_mask": (U64, []),
+    "xd_set_home_mask": (I, [U64]),
+    "xd_home_map_pages": (SZ, [VP, SZ]),
+    "xd_home_map_workspace_size": (SZ, [VP, SZ]),
+    "xd_home_map": (I, [VP, SZ, VP, VP, SZ, VP]),
     "xd_cache_flush_bytes": (SZ, []),
     "xd_cache_flush": (I, [VP, SZ, VP]),
     "xd_gemv_f32": (I, [VP, VP, VP, I, I, I, VP]),
     "xd_gemv_f16f32": (I, [VP, VP, VP, I, I, I, VP]),
     "xd_hist_workspace_size": (SZ, [SZ, U32]),
     "xd_hist_u32": (I, [VP, SZ, VP, U32, I, VP, SZ, VP]),
+    "xd_hash_table_bytes": (SZ, [U64]),
+    "xd_hash_init": (I, [VP, U64, VP]),
+    "xd_hash_insert_u64": (I, [VP, U64, VP, VP, U64, I, VP, VP, VP]),
+    "xd_hash_lookup_u64": (I, [VP, U64, VP, U64, VP, VP, I, VP, VP]),
+    "xd_gen_hash_kv": (I, [VP, VP, U64, U64, VP]),
+    "xd_gen_hash_queries": (I, [VP, U64, U64, U64, U64, VP]),
     "xd_rand64": (U64, [U64, U64]),
     "xd_gen_uniform_f32": (I, [VP, SZ, U64]),
     "xd_gen_normal_f16": (I, [VP, SZ, D, D, U64]),

@@ -1,0 +1,277 @@
+// Open-addressing linear-probe hash table of uint64 keys and uint64 values.
+//
+// Reference: applications/hash/src/hash_probe_dep.cu
+//   Entry{int key; int next}, EMPTY_KEY = -1 (14-21); probe_chain_one (46-64): slot =
+//   mix32(key) & mask, linear probing until the key or EMPTY; probe_dep_base (66-83) walks
+//   queries in launch order (locality-oblivious); probe_dep_sa (85-116) takes per-side query
+//   lists routed on the host (244-270) so that each SM probes slots homed on its L2 side.
+//   The reference builds the table on the CPU (226-241); here insertion is on the GPU.
+//
+// MI355X design. A slot is 16 bytes {key, value}; EMPTY = 0xFFFF'FFFF'FFFF'FFFF; the home
+// slot is mix64(key) & (slots - 1) and probing walks forward with wrap-around. Insert claims
+// a slot with a 64-bit compare-and-swap on the key (executed at the memory side on gfx950)
+// and then stores the value; a lookup reads one 16-byte slot per probe. Placement:
+//   oblivious: keys in input order over a plain grid;
+//   aware:     every workgroup reads the whole input but handles only the keys whose home
+//              slot lies in memory homed on its own I/O die (the slot's address picks the
+//              die, so this partitions the buckets by hash bits), so every probe is a near
+//              access and no routing pass or output scatter is needed;
+//   rotated:   the swapped control: each die handles the keys homed on the other die.
+#include <hip/hip_runtime.h>
+
+#include "xd_common.hpp"
+
+namespace xd {
+
+constexpr uint64_t kEmpty = ~0ull;
+constexpr int kHashThreads = 256;
+constexpr uint64_t kMaxProbe = 1ull << 16;
+
+struct __attribute__((aligned(16))) Slot {
+    uint64_t key;
+    uint64_t val;
+};
+
+__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ void __launch_bounds__(256) hash_init_kernel(Slot *table, uint64_t slots) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < slots; i += stride)
+        table[i] = Slot{kEmpty, 0};
+}
+
+// Work walk. Every wave takes 64-item chunks of the input: chunk c = first + k * stride.
+// Oblivious: the chunks of the whole grid in order. Home modes: the waves of each die walk
+// all chunks (each die sees every item) and keep only the items whose home slot lies on the
+// wanted die; the kept item indices are compacted into a per-wave LDS queue and probed 64
+// at a time, so that no lane idles through a probe loop.
+struct Walk {
+    uint64_t first, stride;  // in 64-item chunks
+    uint32_t want;           // die whose items this wave takes (home modes)
+};
+
+__device__ __forceinline__ Walk make_walk(int mode) {
+    Walk w;
+    const int b = (int)blockIdx.x;
+    const int wave = (int)threadIdx.x / kWave;
+    constexpr int kWavesPerWg = kHashThreads / kWave;
+    if (mode == XD_MODE_OBLIVIOUS) {
+        w.first = (uint64_t)b * kWavesPerWg + wave;
+        w.stride = (uint64_t)gridDim.x * kWavesPerWg;
+        w.want = 0;
+    } else {
+        const int per_die = (int)gridDim.x / 2;
+        const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
+        w.first = (uint64_t)rank * kWavesPerWg + wave;
+        w.stride = (uint64_t)per_die * kWavesPerWg;
+        const uint32_t die = wg_die(b);
+        w.want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
+    }
+    return w;
+}
+
+// Runs body(item) for every item this wave owns, always on a full wave except for the last
+// batch. keep(i) decides ownership (home modes) for item i < n.
+template <typename Keep, typename Body>
+__device__ __forceinline__ void for_each_owned(const Walk &w, uint64_t n, bool filter, uint32_t *queue, Keep keep,
+                                               Body body) {
+    const int lane = lane_id();
+    uint32_t fill = 0;  // wave-uniform
+    for (uint64_t c = w.first; c * kWave < n; c += w.stride) {
+        const uint64_t i = c * kWave + (uint64_t)lane;
+        const bool mine = i < n && (!filter || keep(i));
+        const uint64_t m = __ballot(mine);
+        if (mine) queue[fill + mask_rank(m)] = (uint32_t)i;
+        fill += (uint32_t)__builtin_popcountll(m);
+        __builtin_amdgcn_wave_barrier();
+        if (fill >= (uint32_t)kWave) {
+            const uint32_t item = queue[lane];
+            const uint32_t spill = queue[kWave + lane];
+            body((uint64_t)item);
+            fill -= kWave;
+            if ((uint32_t)lane < fill) queue[lane] = spill;
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    if ((uint32_t)lane < fill) body((uint64_t)queue[lane]);
+}
+
+__global__ void __launch_bounds__(kHashThreads)
+hash_insert_kernel(Slot *__restrict__ table, uint64_t mask, const uint64_t *__restrict__ keys,
+                   const uint64_t *__restrict__ vals, uint64_t n, int mode, HomeMap home,
+                   unsigned long long *__restrict__ failed) {
+    __shared__ uint32_t queues[kHashThreads / kWave][2 * kWave];
+    const Walk w = make_walk(mode);
+    const uint64_t base = reinterpret_cast<uint64_t>(table);
+    const uint64_t max_probe = mask + 1 < kMaxProbe ? mask + 1 : kMaxProbe;
+    auto keep = [&](uint64_t i) {
+        return home(base + (mix64(keys[i]) & mask) * sizeof(Slot)) == w.want;
+    };
+    auto body = [&](uint64_t i) {
+        const uint64_t key = keys[i];
+        if (key == kEmpty) return;
+        const uint64_t val = vals[i];
+        uint64_t s = mix64(key) & mask;
+        for (uint64_t step = 0; step < max_probe; ++step) {
+            unsigned long long *kp = reinterpret_cast<unsigned long long *>(&table[s].key);
+            const uint64_t cur = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint64_t owner = cur;
+            if (cur == kEmpty) owner = atomicCAS(kp, (unsigned long long)kEmpty, (unsigned long long)key);
+            if (owner == kEmpty || owner == key) {
+                table[s].val = val;
+                return;
+            }
+            s = (s + 1) & mask;
+        }
+        if (failed) atomicAdd(failed, 1ull);
+    };
+    for_each_owned(w, n, mode != XD_MODE_OBLIVIOUS, queues[threadIdx.x / kWave], keep, body);
+}
+
+__global__ void __launch_bounds__(kHashThreads)
+hash_lookup_kernel(const Slot *__restrict__ table, uint64_t mask, const uint64_t *__restrict__ queries, uint64_t n,
+                   int mode, HomeMap home, uint64_t *__restrict__ vals_out, uint8_t *__restrict__ found_out) {
+    __shared__ uint32_t queues[kHashThreads / kWave][2 * kWave];
+    const Walk w = make_walk(mode);
+    const uint64_t base = reinterpret_cast<uint64_t>(table);
+    const uint64_t max_probe = mask + 1 < kMaxProbe ? mask + 1 : kMaxProbe;
+    auto keep = [&](uint64_t i) {
+        return home(base + (mix64(queries[i]) & mask) * sizeof(Slot)) == w.want;
+    };
+    auto body = [&](uint64_t i) {
+        const uint64_t q = queries[i];
+        uint64_t s = mix64(q) & mask;
+        uint64_t v = 0;
+        uint8_t f = 0;
+        if (q != kEmpty) {
+            for (uint64_t step = 0; step < max_probe; ++step) {
+                const Slot e = table[s];
+                if (e.key == q) {
+                    v = e.val;
+                    f = 1;
+                    break;
+                }
+                if (e.key == kEmpty) break;
+                s = (s + 1) & mask;
+            }
+        }
+        vals_out[i] = v;
+        found_out[i] = f;
+    };
+    for_each_owned(w, n, mode != XD_MODE_OBLIVIOUS, queues[threadIdx.x / kWave], keep, body);
+}
+
+// Seeded inputs (device): key i = splitmix64(seed, i) (distinct for distinct i),
+// value i = splitmix64(seed ^ 0x5BD1E9955BD1E995, i); query j is a hit for even j
+// (key splitmix64(qseed, j) mod n_keys) and a miss for odd j (key n_keys + j/2, from the
+// disjoint index range above the inserted keys).
+__device__ __forceinline__ uint64_t sm64(uint64_t seed, uint64_t i) { return mix64(seed + (i + 1) * 0x9E3779B97F4A7C15ull); }
+
+__global__ void __launch_bounds__(256) gen_hash_kv_kernel(uint64_t *keys, uint64_t *vals, uint64_t n, uint64_t seed) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        keys[i] = sm64(seed, i);
+        if (vals) vals[i] = sm64(seed ^ 0x5BD1E9955BD1E995ull, i);
+    }
+}
+
+__global__ void __launch_bounds__(256) gen_hash_queries_kernel(uint64_t *q, uint64_t n, uint64_t n_keys, uint64_t seed,
+                                                               uint64_t qseed) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t j = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n; j += stride) {
+        const uint64_t idx = (j & 1) ? n_keys + (j >> 1) : sm64(qseed, j) % n_keys;
+        q[j] = sm64(seed, idx);
+    }
+}
+
+static unsigned grid_for(uint64_t n, unsigned cap) {
+    uint64_t g = (n + 255) / 256;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (unsigned)g;
+}
+
+static int check_table(const void *table, uint64_t slots) {
+    XD_REQUIRE(table != nullptr && aligned16(table), "hash: table must be non-NULL and 16-byte aligned");
+    XD_REQUIRE(slots >= 1 && (slots & (slots - 1)) == 0, "hash: slots must be a power of two");
+    return XD_OK;
+}
+
+// Grid for the probing kernels: a multiple of 8 so that every XCD gets the same number of
+// workgroups (workgroup i runs on XCD i mod 8); 16 workgroups per CU.
+static unsigned probe_grid(uint64_t n) {
+    uint64_t g = (n + kHashThreads - 1) / kHashThreads;
+    const uint64_t cap = 256 * 16;
+    if (g > cap) g = cap;
+    g = (g + kNumXcd - 1) / kNumXcd * kNumXcd;
+    return (unsigned)g;
+}
+
+}  // namespace xd
+
+using namespace xd;
+
+extern "C" {
+
+size_t xd_hash_table_bytes(uint64_t slots) { return (size_t)slots * sizeof(Slot); }
+
+int xd_hash_init(void *table, uint64_t slots, void *stream) {
+    if (int rc = check_table(table, slots)) return rc;
+    KernelTimer kt("hash_init", (hipStream_t)stream);
+    hipLaunchKernelGGL(hash_init_kernel, dim3(grid_for(slots, 8192)), dim3(256), 0, (hipStream_t)stream,
+                       static_cast<Slot *>(table), slots);
+    return launch_status("hash_init_kernel");
+}
+
+int xd_hash_insert_u64(void *table, uint64_t slots, const uint64_t *keys, const uint64_t *vals, uint64_t n, int mode,
+                       const uint8_t *home_attr, unsigned long long *failed, void *stream) {
+    if (int rc = check_table(table, slots)) return rc;
+    XD_REQUIRE(n == 0 || (keys != nullptr && vals != nullptr), "xd_hash_insert_u64: NULL keys/vals");
+    XD_REQUIRE(n < (1ull << 32), "xd_hash_insert_u64: n must be < 2^32 per call");
+    XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_hash_insert_u64: bad mode");
+    if (n == 0) return XD_OK;
+    KernelTimer kt("hash_insert", (hipStream_t)stream);
+    hipLaunchKernelGGL(hash_insert_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+                       static_cast<Slot *>(table), slots - 1, keys, vals, n, mode,
+                       HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()}, failed);
+    return launch_status("hash_insert_kernel");
+}
+
+int xd_hash_lookup_u64(const void *table, uint64_t slots, const uint64_t *queries, uint64_t n, uint64_t *vals_out,
+                       uint8_t *found_out, int mode, const uint8_t *home_attr, void *stream) {
+    if (int rc = check_table(table, slots)) return rc;
+    XD_REQUIRE(n == 0 || (queries != nullptr && vals_out != nullptr && found_out != nullptr),
+               "xd_hash_lookup_u64: NULL queries/outputs");
+    XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_hash_lookup_u64: bad mode");
+    XD_REQUIRE(n < (1ull << 32), "xd_hash_lookup_u64: n must be < 2^32 per call");
+    if (n == 0) return XD_OK;
+    KernelTimer kt("hash_lookup", (hipStream_t)stream);
+    hipLaunchKernelGGL(hash_lookup_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+                       static_cast<const Slot *>(table), slots - 1, queries, n, mode,
+                       HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()}, vals_out,
+                       found_out);
+    return launch_status("hash_lookup_kernel");
+}
+
+int xd_gen_hash_kv(uint64_t *keys, uint64_t *vals, uint64_t n, uint64_t seed, void *stream) {
+    XD_REQUIRE(n == 0 || keys != nullptr, "xd_gen_hash_kv: NULL keys");
+    if (n == 0) return XD_OK;
+    hipLaunchKernelGGL(gen_hash_kv_kernel, dim3(grid_for(n, 8192)), dim3(256), 0, (hipStream_t)stream, keys, vals, n,
+                       seed);
+    return launch_status("gen_hash_kv_kernel");
+}
+
+int xd_gen_hash_queries(uint64_t *queries, uint64_t n, uint64_t n_keys, uint64_t seed, uint64_t qseed, void *stream) {
+    XD_REQUIRE(n == 0 || queries != nullptr, "xd_gen_hash_queries: NULL queries");
+    XD_REQUIRE(n_keys > 0, "xd_gen_hash_queries: n_keys must be positive");
+    if (n == 0) return XD_OK;
+    hipLaunchKernelGGL(gen_hash_queries_kernel, dim3(grid_for(n, 8192)), dim3(256), 0, (hipStream_t)stream, queries, n,
+                       n_keys, seed, qseed);
+    return launch_status("gen_hash_queries_kernel");
+}
+
+}  // extern "C"

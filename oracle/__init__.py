@@ -40,6 +40,11 @@ _SIGS = {
     "ora_zipf_key_at": (U32, [VP, U32, U64, I, U64]),
     "ora_zipf_scramble": (U32, [U32, U32]),
     "ora_histogram": (U64, [VP, SZ, VP, U32, I]),
+    "ora_mix64": (U64, [U64]),
+    "ora_hash_kv": (None, [VP, VP, U64, U64]),
+    "ora_hash_queries": (None, [VP, U64, U64, U64, U64]),
+    "ora_hash_build": (U64, [VP, VP, U64, VP, VP, U64]),
+    "ora_hash_lookup": (None, [VP, VP, U64, VP, U64, VP, VP, I]),
 }
 for _n, (_r, _a) in _SIGS.items():
     _f = getattr(lib, _n)
@@ -130,3 +135,44 @@ def histogram(keys: np.ndarray, num_bins: int, nthreads: int = 1) -> tuple[np.nd
     counts = np.empty(num_bins, dtype=np.uint32)
     c = lib.ora_histogram(_p(keys), keys.size, _p(counts), num_bins, nthreads)
     return counts, int(c)
+
+
+EMPTY = 0xFFFFFFFFFFFFFFFF
+
+
+def mix64(z: int) -> int:
+    return int(lib.ora_mix64(z))
+
+
+def hash_kv(n: int, seed: int):
+    k = np.empty(n, dtype=np.uint64)
+    v = np.empty(n, dtype=np.uint64)
+    lib.ora_hash_kv(_p(k), _p(v), n, seed)
+    return k, v
+
+
+def hash_queries(n: int, n_keys: int, seed: int, qseed: int) -> np.ndarray:
+    q = np.empty(n, dtype=np.uint64)
+    lib.ora_hash_queries(_p(q), n, n_keys, seed, qseed)
+    return q
+
+
+class HashTable:
+    """HASH.cu:226-241 serial insert and HASH.cu:46-64 probing, uint64 keys and values."""
+
+    def __init__(self, slots: int):
+        self.slots = slots
+        self.keys = np.empty(slots, dtype=np.uint64)
+        self.vals = np.empty(slots, dtype=np.uint64)
+
+    def build(self, keys: np.ndarray, vals: np.ndarray) -> int:
+        keys = np.ascontiguousarray(keys, dtype=np.uint64)
+        vals = np.ascontiguousarray(vals, dtype=np.uint64)
+        return int(lib.ora_hash_build(_p(self.keys), _p(self.vals), self.slots, _p(keys), _p(vals), keys.size))
+
+    def lookup(self, q: np.ndarray, nthreads: int = 1):
+        q = np.ascontiguousarray(q, dtype=np.uint64)
+        v = np.empty(q.size, dtype=np.uint64)
+        f = np.empty(q.size, dtype=np.uint8)
+        lib.ora_hash_lookup(_p(self.keys), _p(self.vals), self.slots, _p(q), q.size, _p(v), _p(f), nthreads)
+        return v, f

@@ -293,3 +293,92 @@ uint64_t ora_histogram(const uint32_t *keys, size_t n, uint32_t *counts, uint32_
     }
     return total;
 }
+
+/* ------------------------------------------------------------------------------------ */
+/* hash table                                                                            */
+/* ------------------------------------------------------------------------------------ */
+#define ORA_EMPTY 0xFFFFFFFFFFFFFFFFULL
+
+uint64_t ora_mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+    return z ^ (z >> 31);
+}
+
+void ora_hash_kv(uint64_t *keys, uint64_t *vals, uint64_t n, uint64_t seed) {
+    for (uint64_t i = 0; i < n; ++i) {
+        keys[i] = ora_splitmix64(seed, i);
+        if (vals) vals[i] = ora_splitmix64(seed ^ 0x5bd1e9955bd1e995ULL, i);
+    }
+}
+
+void ora_hash_queries(uint64_t *q, uint64_t n, uint64_t n_keys, uint64_t seed, uint64_t qseed) {
+    for (uint64_t j = 0; j < n; ++j) {
+        uint64_t idx = (j & 1) ? n_keys + (j >> 1) : ora_splitmix64(qseed, j) % n_keys;
+        q[j] = ora_splitmix64(seed, idx);
+    }
+}
+
+static uint64_t probe_limit(uint64_t slots) { return slots < 65536 ? slots : 65536; }
+
+/* HASH.cu:232-241: slot = hash & mask; advance while occupied; store. Here the stored key
+ * may already be the same key (then only the value changes). */
+uint64_t ora_hash_build(uint64_t *tkeys, uint64_t *tvals, uint64_t slots, const uint64_t *keys,
+                        const uint64_t *vals, uint64_t n) {
+    uint64_t mask = slots - 1, failed = 0, lim = probe_limit(slots);
+    for (uint64_t s = 0; s < slots; ++s) {
+        tkeys[s] = ORA_EMPTY;
+        tvals[s] = 0;
+    }
+    for (uint64_t i = 0; i < n; ++i) {
+        uint64_t k = keys[i];
+        if (k == ORA_EMPTY) continue;
+        uint64_t s = ora_mix64(k) & mask, step;
+        for (step = 0; step < lim; ++step) {
+            if (tkeys[s] == ORA_EMPTY || tkeys[s] == k) {
+                tkeys[s] = k;
+                tvals[s] = vals[i];
+                break;
+            }
+            s = (s + 1) & mask;
+        }
+        if (step == lim) failed++;
+    }
+    return failed;
+}
+
+typedef struct {
+    const uint64_t *tkeys, *tvals, *q;
+    uint64_t mask, lim;
+    uint64_t *vals_out;
+    uint8_t *found_out;
+} lookup_ctx;
+
+/* HASH.cu:46-64: probe until the key or EMPTY. */
+static void lookup_range(void *p, int64_t b, int64_t e) {
+    lookup_ctx *c = (lookup_ctx *)p;
+    for (int64_t i = b; i < e; ++i) {
+        uint64_t q = c->q[i], v = 0;
+        uint8_t f = 0;
+        if (q != ORA_EMPTY) {
+            uint64_t s = ora_mix64(q) & c->mask;
+            for (uint64_t step = 0; step < c->lim; ++step) {
+                if (c->tkeys[s] == q) {
+                    v = c->tvals[s];
+                    f = 1;
+                    break;
+                }
+                if (c->tkeys[s] == ORA_EMPTY) break;
+                s = (s + 1) & c->mask;
+            }
+        }
+        c->vals_out[i] = v;
+        c->found_out[i] = f;
+    }
+}
+
+void ora_hash_lookup(const uint64_t *tkeys, const uint64_t *tvals, uint64_t slots, const uint64_t *q,
+                     uint64_t n, uint64_t *vals_out, uint8_t *found_out, int nthreads) {
+    lookup_ctx c = {tkeys, tvals, q, slots - 1, probe_limit(slots), vals_out, found_out};
+    parallel_range((int64_t)n, nthreads, lookup_range, &c);
+}

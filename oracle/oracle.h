@@ -42,4 +42,15 @@ uint32_t ora_zipf_key_at(const uint64_t *t, uint32_t num_bins, uint64_t seed, in
 /* counts[k] = #{i : keys[i] == k}; keys >= num_bins are not counted. Returns the number counted. */
 uint64_t ora_histogram(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int nthreads);
 
+/* ---- hash table (HASH.cu:46-64 probe, HASH.cu:226-241 serial CPU insert; u64 keys+values) ---- */
+uint64_t ora_mix64(uint64_t z); /* splitmix64 output function */
+void ora_hash_kv(uint64_t *keys, uint64_t *vals, uint64_t n, uint64_t seed);
+void ora_hash_queries(uint64_t *q, uint64_t n, uint64_t n_keys, uint64_t seed, uint64_t qseed);
+/* Serial insert in input order into tkeys/tvals (slots entries, tkeys preset by the function
+ * to EMPTY). Returns the number of pairs that found no slot within min(slots, 65536). */
+uint64_t ora_hash_build(uint64_t *tkeys, uint64_t *tvals, uint64_t slots, const uint64_t *keys,
+                        const uint64_t *vals, uint64_t n);
+void ora_hash_lookup(const uint64_t *tkeys, const uint64_t *tvals, uint64_t slots, const uint64_t *q,
+                     uint64_t n, uint64_t *vals_out, uint8_t *found_out, int nthreads);
+
 #endif

@@ -1,0 +1,108 @@
+"""Hash table parity on the GPU: insert + lookup through the C ABI against the oracle's
+serial build (HASH.cu:226-241) and probe (HASH.cu:46-64). found/value bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as ora
+from l2domain_amd.hashtable import (EMPTY, HASH_KEYS, HASH_QSEED, HASH_SEED, HASH_SLOTS, HashTable,
+                                    gen_kv, gen_queries)
+
+pytestmark = pytest.mark.gpu
+MODES = ["oblivious", "aware", "rotated"]
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint64).view(np.int64)).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint64)
+
+
+@pytest.mark.parametrize("ins_mode", MODES)
+@pytest.mark.parametrize("look_mode", MODES)
+def test_small_table_all_mode_pairs(ins_mode, look_mode):
+    slots, n = 1 << 12, 1500
+    keys, vals = ora.hash_kv(n + 600, 11)
+    q = np.concatenate([keys[:n:2], keys[n:], keys[1:n:3]])
+    np.random.default_rng(1).shuffle(q)
+    ref = ora.HashTable(slots)
+    assert ref.build(keys[:n], vals[:n]) == 0
+    rv, rf = ref.lookup(q)
+    t = HashTable(slots)
+    t.insert(dev(keys[:n]), dev(vals[:n]), mode=ins_mode)
+    v, f = t.lookup(dev(q), mode=look_mode)
+    torch.cuda.synchronize()
+    assert t.failures() == 0
+    np.testing.assert_array_equal(f.cpu().numpy(), rf)
+    np.testing.assert_array_equal(host(v), rv)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_full_table_failures_and_reinsert(mode):
+    slots = 1 << 10
+    keys, vals = ora.hash_kv(slots + 50, 5)
+    t = HashTable(slots)
+    t.insert(dev(keys), dev(vals), mode=mode)
+    torch.cuda.synchronize()
+    assert t.failures() == 50  # distinct keys: exactly `slots` of them find a slot
+    _, f = t.lookup(dev(keys), mode=mode)
+    assert int(f.cpu().numpy().sum()) == slots
+    # a fresh table, then the same keys twice: the second pass only updates values
+    t.clear()
+    t.insert(dev(keys[:700]), dev(vals[:700]), mode=mode)
+    t.insert(dev(keys[:700]), dev(vals[::-1][:700]), mode=mode)
+    v, f = t.lookup(dev(keys[:700]), mode=mode)
+    torch.cuda.synchronize()
+    assert t.failures() == 0 and f.cpu().numpy().all()
+    np.testing.assert_array_equal(host(v), vals[::-1][:700])
+
+
+def test_empty_sentinel_and_empty_batches():
+    t = HashTable(1 << 8)
+    k = np.array([EMPTY, 5, 7], dtype=np.uint64)
+    v = np.array([1, 2, 3], dtype=np.uint64)
+    t.insert(dev(k), dev(v))
+    t.insert(dev(k[:0]), dev(v[:0]))
+    vals, f = t.lookup(dev(np.array([EMPTY, 5, 7, 9], dtype=np.uint64)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(f.cpu().numpy(), [0, 1, 1, 0])
+    np.testing.assert_array_equal(host(vals), [0, 2, 3, 0])
+
+
+def test_device_generators_match_oracle():
+    keys, vals = gen_kv(5000, HASH_SEED)
+    q = gen_queries(3000, 5000, HASH_SEED, HASH_QSEED)
+    rk, rv = ora.hash_kv(5000, HASH_SEED)
+    np.testing.assert_array_equal(host(keys), rk)
+    np.testing.assert_array_equal(host(vals), rv)
+    np.testing.assert_array_equal(host(q), ora.hash_queries(3000, 5000, HASH_SEED, HASH_QSEED))
+
+
+@pytest.fixture(scope="module")
+def config_ref():
+    keys, vals = gen_kv(HASH_KEYS, HASH_SEED)
+    q = gen_queries(HASH_KEYS, HASH_KEYS, HASH_SEED, HASH_QSEED)
+    hk, hv, hq = host(keys), host(vals), host(q)
+    assert EMPTY not in set(hk[:1 << 16].tolist())
+    ref = ora.HashTable(HASH_SLOTS)
+    assert ref.build(hk, hv) == 0
+    rv, rf = ref.lookup(hq, nthreads=16)
+    del ref
+    return keys, vals, q, rv, rf
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_config_2p26_insert_lookup(config_ref, mode):
+    keys, vals, q, rv, rf = config_ref
+    assert int(rf.sum()) == HASH_KEYS // 2  # 50% hit rate by construction
+    t = HashTable(HASH_SLOTS)
+    t.insert(keys, vals, mode=mode)
+    v, f = t.lookup(q, mode=mode)
+    torch.cuda.synchronize()
+    assert t.failures() == 0
+    np.testing.assert_array_equal(f.cpu().numpy(), rf)
+    np.testing.assert_array_equal(host(v), rv)
+    del t
+    torch.cuda.empty_cache()

@@ -181,3 +181,66 @@ def test_product_zipf_thresholds_match_oracle():
     from l2domain_amd import gen
     for N, s in ((1 << 20, 1.1), (777, 1.5), (1, 1.1)):
         np.testing.assert_array_equal(gen.zipf_thresholds(N, s), ora.zipf_thresholds(N, s))
+
+
+# ---------------------------------------------------------------------------------------
+# hash table
+# ---------------------------------------------------------------------------------------
+def test_mix64_is_splitmix64_output():
+    # splitmix64(0, 0) = mix64(0x9E3779B97F4A7C15) (published first output for seed 0)
+    assert ora.mix64(0x9E3779B97F4A7C15) == SPLITMIX64_SEED0[0]
+
+
+def test_hash_oracle_matches_python_dict():
+    # Library routine as the reference: a Python dict, with duplicate keys (last value wins).
+    rng = np.random.default_rng(4)
+    keys = rng.integers(0, 2**64 - 1, size=3000, dtype=np.uint64)
+    keys = np.concatenate([keys, keys[:200]])  # duplicates update the value
+    vals = rng.integers(0, 2**64 - 1, size=keys.size, dtype=np.uint64)
+    t = ora.HashTable(1 << 13)
+    assert t.build(keys, vals) == 0
+    d = {}
+    for k, v in zip(keys.tolist(), vals.tolist()):
+        d[k] = v
+    q = np.concatenate([keys[:500], rng.integers(0, 2**64 - 1, size=500, dtype=np.uint64)])
+    got_v, got_f = t.lookup(q, nthreads=2)
+    for k, v, f in zip(q.tolist(), got_v.tolist(), got_f.tolist()):
+        assert f == (k in d)
+        assert v == d.get(k, 0)
+
+
+def test_hash_oracle_linear_probe_invariants():
+    # Every stored key sits at or after its home slot with no EMPTY slot in between.
+    keys, vals = ora.hash_kv(1000, 7)
+    t = ora.HashTable(1 << 11)
+    t.build(keys, vals)
+    mask = t.slots - 1
+    occupied = set(np.nonzero(t.keys != ora.EMPTY)[0].tolist())
+    assert len(occupied) == 1000
+    for s in occupied:
+        k = int(t.keys[s])
+        h = ora.mix64(k) & mask
+        j = h
+        while j != s:
+            assert j in occupied
+            j = (j + 1) & mask
+
+
+def test_hash_oracle_full_table_reports_failures():
+    keys, vals = ora.hash_kv(40, 3)
+    t = ora.HashTable(32)
+    assert t.build(keys, vals) == 8
+    _, f = t.lookup(keys)
+    assert int(f.sum()) == 32
+
+
+def test_hash_generators():
+    n = 1 << 12
+    keys, vals = ora.hash_kv(n + n // 2, 42)
+    assert len(set(keys.tolist())) == keys.size and ora.EMPTY not in set(keys.tolist())
+    q = ora.hash_queries(n, n, 42, 4242)
+    ins = set(keys[:n].tolist())
+    hits = np.array([int(x) in ins for x in q.tolist()])
+    assert hits[0::2].all() and not hits[1::2].any()
+    from l2domain_amd import gen
+    assert gen.rand64(42, 5) == int(keys[5])

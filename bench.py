@@ -288,8 +288,67 @@ class Hash:
                 "sample": "2^23 serial inserts into 2^24 slots + 2^23 lookups (oracle, HASH.cu:46-64,226-241)"}
 
 
+class Bfs:
+    """undirected R-MAT scale 22, edge factor 16, a/b/c/d = .57/.19/.19/.05 (seed
+    8201), CSR int32, source 0. A step = one BFS to completion."""
+    name = "bfs_rmat22_ef16"
+    unit = "GTEPS"
+    dtype = "int32"
+    dominant = "bfs_bottomup"
+
+    def __init__(self):
+        from l2domain_amd.bfs import RMAT_EDGE_FACTOR, RMAT_SCALE, RMAT_SEED, Graph, rmat_csr
+        t0 = time.perf_counter()
+        self.rowptr, self.col = rmat_csr(RMAT_SCALE, RMAT_EDGE_FACTOR, RMAT_SEED)
+        self.gen_s = time.perf_counter() - t0
+        self.g = Graph(self.rowptr, self.col)
+        self.stats = None
+
+    def step(self, mode):
+        _, self.stats = self.g.bfs(0, mode=mode)
+
+    def throughput(self, sec_per_step):
+        return self.stats["reached_edges"] / 2 / sec_per_step / 1e9
+
+    def verify(self):
+        import numpy as np
+        import oracle as ora
+        ref, _ = ora.bfs(self.rowptr, self.col, 0)
+        ok = True
+        for mode in MODES:
+            self.step(mode)
+            ok = ok and bool(np.array_equal(self.g.level.cpu().numpy().view(np.uint32), ref))
+        return ok
+
+    def roofline(self, sec_per_launch):
+        # SURVEY 8(d): 4(V+1) + 4 nnz_reached + 4 V bytes per BFS, attributed to the bottom-up
+        # kernels' share of the run (their summed time per BFS is sec_per_launch * launches)
+        V = self.g.V
+        nbytes = 4 * (V + 1) + 4 * self.stats["reached_edges"] + 4 * V
+        return {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
+                "traffic": None, "kernel": "bfs_bu_kernel", "algorithmic_bytes_per_bfs": nbytes}
+
+    def config(self):
+        return {"workload": self.name, "vertices": self.g.V, "nnz": self.g.nnz, "source": 0, "seed": 8201,
+                "levels": self.stats["levels"] if self.stats else None,
+                "reached_edges": self.stats["reached_edges"] if self.stats else None,
+                "host_generation_s": round(self.gen_s, 2)}
+
+    def cpu_baseline(self):
+        import oracle as ora
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 3.0:
+            ora.bfs(self.rowptr, self.col, 0)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(self.stats["reached_edges"] / 2 / dt / 1e9, 4), "unit": "GTEPS", "cores": 1,
+                "kind": "port", "sample": f"{reps} full serial queue BFS runs of the same graph (oracle)"}
+
+
 WORKLOADS = {
     "hist": Hist,
+    "bfs": Bfs,
     "hash": Hash,
     "gemv_f32": GemvF32,
     "gemv_f16_up": lambda: GemvF16(14336, 4096),

@@ -205,6 +205,35 @@ int xd_gen_hash_queries(uint64_t *queries, uint64_t n, uint64_t n_keys, uint64_t
                         void *stream);
 
 /* ------------------------------------------------------------------------------------ */
+/* BFS over an undirected CSR graph                                                       */
+/* ------------------------------------------------------------------------------------ */
+typedef struct {
+    int32_t levels;           /* distinct BFS levels (max level + 1)                    */
+    int32_t topdown_steps;
+    int32_t bottomup_steps;
+    int64_t reached_vertices;
+    int64_t reached_edges;    /* sum of the degrees of the reached vertices (TEPS = /2) */
+} xd_bfs_stats_t;
+
+size_t xd_bfs_workspace_size(int32_t num_vertices, int64_t nnz);
+
+/* level[v] = BFS distance from src, XD_BFS_UNVISITED (0xFFFFFFFF) if unreachable, for the
+ * undirected graph rowptr[V+1] / col[nnz] (int32, device; every edge stored both ways).
+ * Direction-optimizing (top-down queue steps, bottom-up bitmap steps, Beamer's switch with
+ * alpha = 14 and beta = 24). Synchronous: the host reads two counters per level. Replaces
+ * luo_baseline_level_kernel / luo_side_level_kernel and the host level loops
+ * (applications/bfs/src/bfs.cu:215-308, 449-491), which run a fixed number of top-down
+ * levels from many sources; the level values follow the same rule (depth + 1 at the first
+ * claim, :240, 0xFFFFFFFF unvisited, :30). Modes act on the bottom-up steps:
+ * XD_MODE_OBLIVIOUS walks 64-vertex blocks in order; XD_MODE_AWARE gives each I/O die the
+ * 64-vertex blocks whose adjacency starts in col memory homed on that die (home_attr =
+ * xd_home_map() of col, optional); XD_MODE_ROTATED gives each die the other die's blocks. */
+#define XD_BFS_UNVISITED 0xFFFFFFFFu
+int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t num_vertices, int64_t nnz, int32_t src,
+               uint32_t *level, int mode, const uint8_t *home_attr, void *workspace, size_t workspace_bytes,
+               void *stream, xd_bfs_stats_t *stats);
+
+/* ------------------------------------------------------------------------------------ */
 /* Seeded input generators (host). Fully specified integer mixers; no libc RNG.          */
 /* ------------------------------------------------------------------------------------ */
 
@@ -227,6 +256,19 @@ int xd_zipf_thresholds(uint64_t *out, uint32_t num_bins, double s);
  * ranks are spread over the bin range; otherwise bin = rank. Enqueued on `stream`. */
 int xd_gen_zipf_keys(uint32_t *keys, size_t n, const uint64_t *thresholds, uint32_t num_bins,
                      uint64_t seed, int scramble, void *stream);
+
+/* R-MAT edge e of a 2^scale-vertex graph (host): `scale` quadrant draws, most significant
+ * bit first; draw l uses 32-bit word (l & 1) (low word first) of
+ * xd_rand64(seed, e * ceil(scale/2) + l/2) against floor(a * 2^32), floor((a+b) * 2^32),
+ * floor((a+b+c) * 2^32); quadrants c, d set the row bit and b, d the column bit. */
+int xd_rmat_edge(int scale, double a, double b, double c, uint64_t seed, uint64_t e, int32_t *u,
+                 int32_t *v);
+
+/* Undirected CSR of the R-MAT graph with edge_factor * 2^scale edges (host buffers): every
+ * edge (u, v), u != v, in both directions, duplicates removed, lists sorted ascending.
+ * rowptr has 2^scale + 1 entries; col needs capacity >= 2 * edge_factor * 2^scale. */
+int xd_rmat_csr(int scale, int edge_factor, double a, double b, double c, uint64_t seed, int32_t *rowptr,
+                int32_t *col, int64_t col_capacity, int64_t *nnz_out);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,11 @@ class XdomError(RuntimeError):
         self.code = code
 
 
+class BfsStats(C.Structure):
+    _fields_ = [("levels", C.c_int32), ("topdown_steps", C.c_int32), ("bottomup_steps", C.c_int32),
+                ("reached_vertices", C.c_int64), ("reached_edges", C.c_int64)]
+
+
 class Topology(C.Structure):
     _fields_ = [("device", C.c_int), ("num_cu", C.c_int), ("num_xcd", C.c_int),
                 ("cu_per_xcd", C.c_int), ("wave_size", C.c_int), ("clock_khz", C.c_int),
@@ -77,11 +82,15 @@ SIGNATURES: dict[str, tuple] = {
     "xd_hash_lookup_u64": (I, [VP, U64, VP, U64, VP, VP, I, VP, VP]),
     "xd_gen_hash_kv": (I, [VP, VP, U64, U64, VP]),
     "xd_gen_hash_queries": (I, [VP, U64, U64, U64, U64, VP]),
+    "xd_bfs_workspace_size": (SZ, [C.c_int32, I64]),
+    "xd_bfs_csr": (I, [VP, VP, C.c_int32, I64, C.c_int32, VP, I, VP, VP, SZ, VP, C.POINTER(BfsStats)]),
     "xd_rand64": (U64, [U64, U64]),
     "xd_gen_uniform_f32": (I, [VP, SZ, U64]),
     "xd_gen_normal_f16": (I, [VP, SZ, D, D, U64]),
     "xd_zipf_thresholds": (I, [VP, U32, D]),
     "xd_gen_zipf_keys": (I, [VP, SZ, VP, U32, U64, I, VP]),
+    "xd_rmat_edge": (I, [I, D, D, D, U64, U64, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    "xd_rmat_csr": (I, [I, I, D, D, D, U64, VP, VP, I64, C.POINTER(I64)]),
 }
 
 

@@ -45,6 +45,9 @@ _SIGS = {
     "ora_hash_queries": (None, [VP, U64, U64, U64, U64]),
     "ora_hash_build": (U64, [VP, VP, U64, VP, VP, U64]),
     "ora_hash_lookup": (None, [VP, VP, U64, VP, U64, VP, VP, I]),
+    "ora_rmat_edge": (None, [I, D, D, D, U64, U64, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
+    "ora_rmat_csr": (I64, [I, I, D, D, D, U64, VP, VP]),
+    "ora_bfs": (I64, [VP, VP, C.c_int32, C.c_int32, VP]),
 }
 for _n, (_r, _a) in _SIGS.items():
     _f = getattr(lib, _n)
@@ -176,3 +179,30 @@ class HashTable:
         f = np.empty(q.size, dtype=np.uint8)
         lib.ora_hash_lookup(_p(self.keys), _p(self.vals), self.slots, _p(q), q.size, _p(v), _p(f), nthreads)
         return v, f
+
+
+RMAT_ABC = (0.57, 0.19, 0.19)
+
+
+def rmat_edge(scale: int, seed: int, e: int, abc=RMAT_ABC) -> tuple[int, int]:
+    u, v = C.c_int32(), C.c_int32()
+    lib.ora_rmat_edge(scale, *abc, seed, e, C.byref(u), C.byref(v))
+    return u.value, v.value
+
+
+def rmat_csr(scale: int, edge_factor: int, seed: int, abc=RMAT_ABC):
+    V = 1 << scale
+    rowptr = np.empty(V + 1, dtype=np.int32)
+    col = np.empty(2 * edge_factor * V, dtype=np.int32)
+    nnz = int(lib.ora_rmat_csr(scale, edge_factor, *abc, seed, _p(rowptr), _p(col)))
+    return rowptr, col[:nnz].copy()
+
+
+def bfs(rowptr: np.ndarray, col: np.ndarray, src: int):
+    """Serial queue BFS: (level u32[V], number reached)."""
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    col = np.ascontiguousarray(col, dtype=np.int32)
+    V = rowptr.size - 1
+    level = np.empty(V, dtype=np.uint32)
+    n = int(lib.ora_bfs(_p(rowptr), _p(col) if col.size else None, V, src, _p(level)))
+    return level, n

@@ -382,3 +382,88 @@ void ora_hash_lookup(const uint64_t *tkeys, const uint64_t *tvals, uint64_t slot
     lookup_ctx c = {tkeys, tvals, q, slots - 1, probe_limit(slots), vals_out, found_out};
     parallel_range((int64_t)n, nthreads, lookup_range, &c);
 }
+
+/* ------------------------------------------------------------------------------------ */
+/* R-MAT and BFS                                                                         */
+/* ------------------------------------------------------------------------------------ */
+void ora_rmat_edge(int scale, double a, double b, double c, uint64_t seed, uint64_t e, int32_t *u, int32_t *v) {
+    uint32_t ta = (uint32_t)floor(a * 4294967296.0), tab = (uint32_t)floor((a + b) * 4294967296.0),
+             tabc = (uint32_t)floor((a + b + c) * 4294967296.0);
+    uint64_t words = (uint64_t)(scale + 1) / 2;
+    uint32_t uu = 0, vv = 0;
+    for (int l = 0; l < scale; ++l) {
+        uint64_t w = ora_splitmix64(seed, e * words + (uint64_t)(l / 2));
+        uint32_t r = (l & 1) ? (uint32_t)(w >> 32) : (uint32_t)w;
+        int row = r >= tab;            /* quadrants c, d */
+        int colb = (r >= ta && r < tab) || r >= tabc; /* quadrants b, d */
+        uu = (uu << 1) | (uint32_t)row;
+        vv = (vv << 1) | (uint32_t)colb;
+    }
+    *u = (int32_t)uu;
+    *v = (int32_t)vv;
+}
+
+static int cmp_i32(const void *x, const void *y) {
+    int32_t a = *(const int32_t *)x, b = *(const int32_t *)y;
+    return (a > b) - (a < b);
+}
+
+int64_t ora_rmat_csr(int scale, int edge_factor, double a, double b, double c, uint64_t seed, int32_t *rowptr,
+                     int32_t *col) {
+    int64_t V = (int64_t)1 << scale, E = (int64_t)edge_factor * V;
+    int64_t *deg = (int64_t *)calloc((size_t)V + 1, sizeof(int64_t));
+    int32_t *eu = (int32_t *)malloc(sizeof(int32_t) * (size_t)E), *ev = (int32_t *)malloc(sizeof(int32_t) * (size_t)E);
+    for (int64_t e = 0; e < E; ++e) {
+        ora_rmat_edge(scale, a, b, c, seed, (uint64_t)e, &eu[e], &ev[e]);
+        if (eu[e] != ev[e]) {
+            deg[eu[e]]++;
+            deg[ev[e]]++;
+        }
+    }
+    int64_t *off = (int64_t *)malloc(sizeof(int64_t) * ((size_t)V + 1)), *fill = (int64_t *)calloc((size_t)V, sizeof(int64_t));
+    off[0] = 0;
+    for (int64_t i = 0; i < V; ++i) off[i + 1] = off[i] + deg[i];
+    int32_t *tmp = (int32_t *)malloc(sizeof(int32_t) * (size_t)(off[V] > 0 ? off[V] : 1));
+    for (int64_t e = 0; e < E; ++e)
+        if (eu[e] != ev[e]) {
+            tmp[off[eu[e]] + fill[eu[e]]++] = ev[e];
+            tmp[off[ev[e]] + fill[ev[e]]++] = eu[e];
+        }
+    int64_t n = 0;
+    rowptr[0] = 0;
+    for (int64_t v = 0; v < V; ++v) {
+        int64_t len = off[v + 1] - off[v];
+        qsort(tmp + off[v], (size_t)len, sizeof(int32_t), cmp_i32);
+        for (int64_t j = 0; j < len; ++j)
+            if (j == 0 || tmp[off[v] + j] != tmp[off[v] + j - 1]) col[n++] = tmp[off[v] + j];
+        rowptr[v + 1] = (int32_t)n;
+    }
+    free(deg);
+    free(eu);
+    free(ev);
+    free(off);
+    free(fill);
+    free(tmp);
+    return n;
+}
+
+/* Textbook BFS with a FIFO queue; level = depth of first discovery (bfs.cu:240, :30). */
+int64_t ora_bfs(const int32_t *rowptr, const int32_t *col, int32_t V, int32_t src, uint32_t *level) {
+    for (int32_t v = 0; v < V; ++v) level[v] = 0xffffffffu;
+    int32_t *q = (int32_t *)malloc(sizeof(int32_t) * (size_t)V);
+    int64_t head = 0, tail = 0;
+    level[src] = 0;
+    q[tail++] = src;
+    while (head < tail) {
+        int32_t u = q[head++];
+        for (int32_t e = rowptr[u]; e < rowptr[u + 1]; ++e) {
+            int32_t v = col[e];
+            if (level[v] == 0xffffffffu) {
+                level[v] = level[u] + 1;
+                q[tail++] = v;
+            }
+        }
+    }
+    free(q);
+    return tail;
+}

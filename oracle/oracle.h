@@ -53,4 +53,13 @@ uint64_t ora_hash_build(uint64_t *tkeys, uint64_t *tvals, uint64_t slots, const 
 void ora_hash_lookup(const uint64_t *tkeys, const uint64_t *tvals, uint64_t slots, const uint64_t *q,
                      uint64_t n, uint64_t *vals_out, uint8_t *found_out, int nthreads);
 
+/* ---- BFS (bfs.cu:215-252 level rule: depth + 1 at the first visit, 0xFFFFFFFF unvisited) ---- */
+void ora_rmat_edge(int scale, double a, double b, double c, uint64_t seed, uint64_t e, int32_t *u, int32_t *v);
+/* Undirected CSR (both directions, no self-loops, no duplicates, sorted lists); returns nnz.
+ * col must hold 2 * edge_factor * 2^scale entries. */
+int64_t ora_rmat_csr(int scale, int edge_factor, double a, double b, double c, uint64_t seed, int32_t *rowptr,
+                     int32_t *col);
+/* Serial FIFO-queue BFS; returns the number of reached vertices. */
+int64_t ora_bfs(const int32_t *rowptr, const int32_t *col, int32_t V, int32_t src, uint32_t *level);
+
 #endif

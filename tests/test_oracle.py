@@ -244,3 +244,55 @@ def test_hash_generators():
     assert hits[0::2].all() and not hits[1::2].any()
     from l2domain_amd import gen
     assert gen.rand64(42, 5) == int(keys[5])
+
+
+# ---------------------------------------------------------------------------------------
+# R-MAT and BFS
+# ---------------------------------------------------------------------------------------
+def test_bfs_oracle_matches_scipy_shortest_path():
+    from scipy.sparse import csr_matrix
+    from scipy.sparse.csgraph import shortest_path
+    rowptr, col = ora.rmat_csr(10, 8, 8201)
+    V = rowptr.size - 1
+    A = csr_matrix((np.ones(col.size), col, rowptr), shape=(V, V))
+    for src in (0, 5, 777):
+        level, reached = ora.bfs(rowptr, col, src)
+        d = shortest_path(A, method="D", unweighted=True, indices=src)
+        ref = np.where(np.isinf(d), 0xFFFFFFFF, d).astype(np.uint32)
+        np.testing.assert_array_equal(level, ref)
+        assert reached == int(np.isfinite(d).sum())
+
+
+def test_rmat_csr_is_a_simple_undirected_graph():
+    rowptr, col = ora.rmat_csr(9, 16, 1)
+    V = rowptr.size - 1
+    pairs = set()
+    for u in range(V):
+        nb = col[rowptr[u]:rowptr[u + 1]]
+        assert np.all(np.diff(nb) > 0)  # sorted, no duplicates
+        assert u not in set(nb.tolist())  # no self loops
+        pairs.update((u, int(v)) for v in nb)
+    assert all((v, u) in pairs for (u, v) in pairs)  # symmetric
+
+
+def test_rmat_edges_follow_quadrant_probabilities():
+    # one level: P(row bit = 1) = c + d = 0.24, P(col bit = 1) = b + d = 0.24
+    n = 20000
+    rows = cols = 0
+    for e in range(n):
+        u, v = ora.rmat_edge(1, 3, e)
+        rows += u
+        cols += v
+    assert abs(rows / n - 0.24) < 0.012 and abs(cols / n - 0.24) < 0.012
+    # the top 1/8 of ids at scale 3 is reached with probability (c + d)^3 ~ 1.4 %
+    hits = sum(1 for e in range(n) if ora.rmat_edge(3, 9, e)[0] == 7)
+    assert abs(hits / n - 0.24 ** 3) < 0.004
+
+
+def test_product_rmat_matches_oracle():
+    from l2domain_amd.bfs import rmat_csr
+    for scale, ef, seed in ((8, 16, 8201), (11, 4, 3)):
+        r1, c1 = rmat_csr(scale, ef, seed)
+        r2, c2 = ora.rmat_csr(scale, ef, seed)
+        np.testing.assert_array_equal(r1, r2)
+        np.testing.assert_array_equal(c1, c2)

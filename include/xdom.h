@@ -136,13 +136,19 @@ int xd_cache_flush(const void *buf, size_t bytes, void *stream);
 /* fp32 GEMV. Replaces gemv_partitioned_kernel / gemv_baseline_kernel
  * (applications/gemv/src/gemv_k1024_persistent_subwarp.cu:163-231), generalised from the
  * compile-time K=1024 to any K with K % 4 == 0 and 16-byte aligned A and x.
- * Writes every y[i] (no accumulation into y). */
-int xd_gemv_f32(const float *A, const float *x, float *y, int M, int K, int mode, void *stream);
+ * Writes every y[i] (no accumulation into y). Placement: XD_MODE_OBLIVIOUS hands row
+ * chunks to workgroups in order (consecutive chunks land on different XCDs); XD_MODE_AWARE
+ * routes each row to the I/O die homing it when rows do not straddle 8 KiB chunks (row
+ * bytes divide 8192 and A is 8 KiB aligned; home_attr = xd_home_map() of A, optional), and
+ * otherwise gives every XCD one contiguous eighth of the rows (the reference's per-side
+ * row lists, GEMV.cu:264-273); XD_MODE_ROTATED is the far-die / next-XCD control. */
+int xd_gemv_f32(const float *A, const float *x, float *y, int M, int K, int mode, const uint8_t *home_attr,
+                void *stream);
 
 /* fp16 weights and vector (IEEE binary16 bit patterns), fp32 accumulation, fp32 y.
  * Same structure as xd_gemv_f32; K % 8 == 0, 16-byte aligned W and x. */
 int xd_gemv_f16f32(const uint16_t *W, const uint16_t *x, float *y, int M, int K, int mode,
-                   void *stream);
+                   const uint8_t *home_attr, void *stream);
 
 /* ------------------------------------------------------------------------------------ */
 /* Histogram  counts[k] = #{i : keys[i] == k}, k < num_bins                               */

@@ -174,6 +174,56 @@ gemv_exact_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, floa
     }
 }
 
+// Memory-home variant for rows that never straddle an 8 KiB chunk (row bytes divide 8 KiB,
+// A 8 KiB aligned): each row lives on one I/O die, and the workgroups of a die take only
+// the rows homed on the wanted die (aware: their own die; rotated: the other one). Rows are
+// visited in groups of 8 consecutive rows; lane i of every wave evaluates the home of row
+// 8g + i, and the waves of the workgroup split the group's matching rows among them.
+template <bool F16, int CW>
+__global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4)))
+gemv_rowhome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__restrict__ y, int M,
+                    int mode, HomeMap home) {
+    constexpr int nv = kWave * CW;
+    constexpr int kGroup = 8;
+    extern __shared__ uint4 xs[];
+    const int b = (int)blockIdx.x;
+    const int per_die = (int)gridDim.x / 2;
+    const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
+    const uint32_t die = wg_die(b);
+    const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
+    const int wave = (int)threadIdx.x / kWave;
+    const int lane = (int)threadIdx.x % kWave;
+    for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
+    __syncthreads();
+    const uint64_t abase = reinterpret_cast<uint64_t>(A);
+    const int ngroups = (M + kGroup - 1) / kGroup;
+    for (int g = rank; g < ngroups; g += per_die) {
+        const int r = g * kGroup + lane;
+        const bool mine = lane < kGroup && r < M && home(abase + (uint64_t)r * nv * 16) == want;
+        uint64_t m = __ballot(mine);
+        // drop the first `wave` matching rows, then take every kGemvWaves-th one
+        for (int k = 0; k < wave && m; ++k) m &= m - 1;
+        while (m) {
+            const int row = g * kGroup + __builtin_ctzll(m);
+            const uint4 *p = A + (size_t)row * nv + lane;
+            uint4 a[CW];
+#pragma unroll
+            for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
+            float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+            for (int u = 0; u < CW; u += 2) {
+                acc0 = F16 ? dot16_f16(a[u], xs[u * kWave + lane], acc0) : dot16_f32(a[u], xs[u * kWave + lane], acc0);
+                if (u + 1 < CW)
+                    acc1 = F16 ? dot16_f16(a[u + 1], xs[(u + 1) * kWave + lane], acc1)
+                               : dot16_f32(a[u + 1], xs[(u + 1) * kWave + lane], acc1);
+            }
+            const float acc = wave_sum_f32(acc0 + acc1);
+            if (lane == 0) y[row] = acc;
+            for (int k = 0; k < kGemvWaves && m; ++k) m &= m - 1;
+        }
+    }
+}
+
 static int rows_per_workgroup(int M, int nv) {
     // XD_GEMV_ROWS_PER_WG overrides the heuristic (tuning sweeps); must be a multiple of 4.
     if (const char *e = getenv("XD_GEMV_ROWS_PER_WG")) {
@@ -187,7 +237,8 @@ static int rows_per_workgroup(int M, int nv) {
 }
 
 template <bool F16>
-static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int mode, void *stream) {
+static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int mode, const uint8_t *home_attr,
+                       void *stream) {
     const int per_vec = F16 ? 8 : 4;
     XD_REQUIRE(A != nullptr && x != nullptr && y != nullptr, "gemv: NULL pointer");
     XD_REQUIRE(M > 0 && K > 0, "gemv: M and K must be positive");
@@ -206,7 +257,29 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
     const uint4 *x4 = reinterpret_cast<const uint4 *>(x);
     KernelTimer kt(F16 ? "gemv_f16f32" : "gemv_f32", s);
     bool done = false;
-    if (nv % kWave == 0) {
+    // Memory-home routing when every row sits inside one 8 KiB chunk.
+    const size_t row_bytes = (size_t)nv * 16;
+    if (mode != XD_MODE_OBLIVIOUS && kHomeChunk % row_bytes == 0 && (reinterpret_cast<uintptr_t>(A) % kHomeChunk) == 0 &&
+        nv % kWave == 0) {
+        const int CW = nv / kWave;
+        const HomeMap home{home_attr, reinterpret_cast<uint64_t>(A) / kHomePage, home_mask()};
+        // two groups of 8 rows per workgroup on average
+        int hgrid = ((M + 15) / 16 + kNumXcd - 1) / kNumXcd * kNumXcd;
+        if (hgrid < kNumXcd) hgrid = kNumXcd;
+        done = true;
+#define XD_GEMV_HOME(CC)                                                                                       \
+    if (CW == CC) {                                                                                           \
+        hipLaunchKernelGGL((gemv_rowhome_kernel<F16, CC>), dim3(hgrid), dim3(kGemvThreads), lds, s, A4, x4, y, M, \
+                           mode, home);                                                                        \
+    } else
+        XD_GEMV_HOME(1)
+        XD_GEMV_HOME(2)
+        XD_GEMV_HOME(4)
+        XD_GEMV_HOME(8)
+        { done = false; }
+#undef XD_GEMV_HOME
+    }
+    if (!done && nv % kWave == 0) {
         // smallest split S (1, 2, 4) with at most 8 vectors per lane per wave
         const int C = nv / kWave;
         int S = 1;
@@ -255,12 +328,14 @@ using namespace xd;
 
 extern "C" {
 
-int xd_gemv_f32(const float *A, const float *x, float *y, int M, int K, int mode, void *stream) {
-    return launch_gemv<false>(A, x, y, M, K, mode, stream);
+int xd_gemv_f32(const float *A, const float *x, float *y, int M, int K, int mode, const uint8_t *home_attr,
+                void *stream) {
+    return launch_gemv<false>(A, x, y, M, K, mode, home_attr, stream);
 }
 
-int xd_gemv_f16f32(const uint16_t *W, const uint16_t *x, float *y, int M, int K, int mode, void *stream) {
-    return launch_gemv<true>(W, x, y, M, K, mode, stream);
+int xd_gemv_f16f32(const uint16_t *W, const uint16_t *x, float *y, int M, int K, int mode, const uint8_t *home_attr,
+                   void *stream) {
+    return launch_gemv<true>(W, x, y, M, K, mode, home_attr, stream);
 }
 
 }  // extern "C"

@@ -13,8 +13,9 @@ from ._torch import mode_id, ptr, stream_handle
 
 
 def gemv(A: torch.Tensor, x: torch.Tensor, y: torch.Tensor | None = None, mode="aware",
-         stream: torch.cuda.Stream | None = None) -> torch.Tensor:
-    """y[M] (fp32) = A[M,K] . x[K]. A/x are both float32 or both float16."""
+         stream: torch.cuda.Stream | None = None, home_attr: torch.Tensor | None = None) -> torch.Tensor:
+    """y[M] (fp32) = A[M,K] . x[K]. A/x are both float32 or both float16. home_attr: the
+    xd_home_map of A (domain.home_map(A)); used by the aware/rotated modes only."""
     if A.dim() != 2 or x.dim() != 1 or A.shape[1] != x.shape[0]:
         raise ValueError("gemv: expected A[M,K] and x[K]")
     M, K = A.shape
@@ -23,9 +24,10 @@ def gemv(A: torch.Tensor, x: torch.Tensor, y: torch.Tensor | None = None, mode="
     if y.dtype != torch.float32 or y.numel() != M:
         raise ValueError("gemv: y must be float32[M]")
     if A.dtype == torch.float32 and x.dtype == torch.float32:
-        _lib.call("xd_gemv_f32", ptr(A), ptr(x), ptr(y), M, K, mode_id(mode), stream_handle(stream))
+        _lib.call("xd_gemv_f32", ptr(A), ptr(x), ptr(y), M, K, mode_id(mode), ptr(home_attr), stream_handle(stream))
     elif A.dtype == torch.float16 and x.dtype == torch.float16:
-        _lib.call("xd_gemv_f16f32", ptr(A), ptr(x), ptr(y), M, K, mode_id(mode), stream_handle(stream))
+        _lib.call("xd_gemv_f16f32", ptr(A), ptr(x), ptr(y), M, K, mode_id(mode), ptr(home_attr),
+                  stream_handle(stream))
     else:
         raise TypeError("gemv: A and x must both be float32 or both float16")
     return y

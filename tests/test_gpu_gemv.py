@@ -18,11 +18,15 @@ pytestmark = pytest.mark.gpu
 MODES = ["oblivious", "aware", "rotated"]
 
 
-def run(A: np.ndarray, x: np.ndarray, mode) -> np.ndarray:
+def run(A: np.ndarray, x: np.ndarray, mode, mapped: bool = False) -> np.ndarray:
     dA = torch.from_numpy(np.ascontiguousarray(A)).cuda()
     dx = torch.from_numpy(np.ascontiguousarray(x)).cuda()
     y = torch.full((A.shape[0],), float("nan"), dtype=torch.float32, device="cuda")
-    gemv(dA, dx, y, mode=mode)
+    home = None
+    if mapped:
+        from l2domain_amd.domain import home_map
+        home = home_map(dA)
+    gemv(dA, dx, y, mode=mode, home_attr=home)
     torch.cuda.synchronize()
     return y.cpu().numpy()
 
@@ -84,10 +88,11 @@ def f16_config(request):
     return W, x, ref, yabs
 
 
+@pytest.mark.parametrize("mapped", [False, True], ids=["maskhome", "mappedhome"])
 @pytest.mark.parametrize("mode", MODES)
-def test_f16_decode_shapes(f16_config, mode):
+def test_f16_decode_shapes(f16_config, mode, mapped):
     W, x, ref, yabs = f16_config
-    y = run(W, x, mode)
+    y = run(W, x, mode, mapped)
     assert np.all(np.isfinite(y))
     assert rel_err(y, ref) <= 2e-2
     assert np.all(np.abs(y - ref) <= 2e-2 * yabs)
@@ -111,3 +116,23 @@ def test_f16_integer_inputs_exact():
     ref = (W.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)
     for mode in MODES:
         np.testing.assert_array_equal(run(W, x, mode), ref)
+
+
+def test_f16_row_home_modes_bit_identical():
+    # up-projection rows are 8 KiB: the aware/rotated modes route whole rows by home die and
+    # must reproduce the oblivious kernel bit for bit (same per-row summation order)
+    W, x = gen.gemv_f16_inputs(14336, 4096)
+    ys = [run(W, x, m, mapped=True) for m in MODES]
+    for y in ys[1:]:
+        np.testing.assert_array_equal(ys[0].view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K", [(1, 4096), (7, 4096), (333, 2048), (100, 512), (9, 64)])
+def test_f16_row_home_ragged(M, K):
+    # row bytes 8192, 4096, 1024, 128 all divide 8 KiB: the home-routed kernel is used
+    W, x = gen.gemv_f16_inputs(M, K, w_seed=M + K, x_seed=K)
+    ref, yabs = ora.gemv_f64(W, x)
+    for mode in MODES:
+        y = run(W, x, mode, mapped=True)
+        assert rel_err(y, ref) <= 2e-2
+        assert np.all(np.abs(y - ref) <= 2e-2 * yabs + 1e-30)

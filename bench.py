@@ -1,13 +1,15 @@
 #!/usr/bin/env python3
 """Benchmark of the XCD-domain kernels on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--all]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--cold] [--only] [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input already resident in
 HBM: one GEMV call, one histogram of 2^28 keys, ... W untimed warm-up steps, then exactly K
 steps timed with HIP events on the stream the kernels are launched on. Prints ONE JSON line.
 `value` is the XCD-aware variant's throughput; the oblivious and rotated variants are
 timed over the same K steps and reported beside it with the aware/oblivious speedup.
+Unless --only is given, every other configuration (GEMV fp32 and fp16 warm and cold, hash,
+BFS) is measured the same way, with at most 50 timed steps, under "extras".
 """
 from __future__ import annotations
 
@@ -38,6 +40,8 @@ def _cpu_threads() -> int:
 # Workloads
 # ---------------------------------------------------------------------------------------
 class GemvF32:
+    single_kernel = True  # a step is exactly one launch: the timed region gives its duration
+
     """configs[0]: fp32 y = A.x, A 4096x4096 and x from U[-1,1) (seed 4242)."""
     name = "gemv_f32_4096x4096"
     unit = "GB/s"
@@ -194,10 +198,13 @@ class Hist:
         return ok
 
     def roofline(self, sec_per_launch):
-        # dominant kernel: the partition pass; its algorithmic traffic is the 4 B/key read
+        # dominant kernel: the partition pass; its algorithmic traffic is the 4 B/key read.
+        # traffic: rocprofv3 --pmc FETCH_SIZE (x2.000, copy-kernel calibration) + WRITE_SIZE of
+        # this kernel at this configuration: 1,073,846,600 B read + 541,589,504 B written.
         achieved = 4 * self.n / sec_per_launch / 1e9
+        traffic = 1615436104 if (self.n, self.num_bins) == (1 << 28, 1 << 20) else None
         return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "hist_partition_kernel",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "hist_partition_kernel",
                 "algorithmic_bytes_per_launch": 4 * self.n}
 
     def op_roofline(self, sec_per_step):
@@ -216,7 +223,7 @@ class Hist:
         sample = self._host[: 1 << 26] if hasattr(self, "_host") else self.keys[: 1 << 26].cpu().numpy().view(np.uint32)
         t0 = time.perf_counter()
         reps = 0
-        while time.perf_counter() - t0 < 5.0:
+        while time.perf_counter() - t0 < 10.0:
             ora.histogram(sample, self.num_bins, nthreads=nt)
             reps += 1
         dt = (time.perf_counter() - t0) / reps
@@ -362,6 +369,9 @@ WORKLOADS = {
     "gemv_f16_down": lambda: GemvF16(4096, 14336),
 }
 DEFAULT_WORKLOAD = "hist"
+# every other BASELINE config, reported under "extras" of the same JSON line
+EXTRAS = (("gemv_f32", False), ("gemv_f32", True), ("gemv_f16_up", False), ("gemv_f16_up", True),
+          ("gemv_f16_down", False), ("gemv_f16_down", True), ("hash", False), ("bfs", False))
 
 
 # ---------------------------------------------------------------------------------------
@@ -413,6 +423,15 @@ def kernel_times(wl, mode, steps, flusher=None):
     return {k: (ms / 1e3 / max(n, 1), n) for k, (ms, n) in t.items()}
 
 
+def launch_seconds(wl, r):
+    """Average duration of the dominant kernel in the aware mode. A one-kernel step is timed by
+    the back-to-back timed region (per-launch events would add their own overhead to a ~10 us
+    kernel); otherwise by the library's HIP events around that kernel."""
+    if getattr(wl, "single_kernel", False):
+        return r["sec"]["aware"]
+    return r["kernels"][wl.dominant][0]
+
+
 def run_workload(name, steps, warmup, cold=False, with_cpu=True):
     import torch
     from l2domain_amd.domain import CacheFlusher
@@ -445,7 +464,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--cold", action="store_true", help="flush L2 + Infinity Cache before every step")
-    ap.add_argument("--all", action="store_true", help="also measure every other workload (extras)")
+    ap.add_argument("--only", action="store_true", help="measure the selected workload only (no extras)")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
 
@@ -483,7 +502,7 @@ def main():
                   for m in MODES},
         "speedup_aware_vs_oblivious": round(r["sec"]["oblivious"] / r["sec"]["aware"], 4),
         "speedup_rotated_vs_oblivious": round(r["sec"]["oblivious"] / r["sec"]["rotated"], 4),
-        "roofline": wl.roofline(r["kernels"][wl.dominant][0]),
+        "roofline": wl.roofline(launch_seconds(wl, r)),
         "kernels_us": {k: round(v[0] * 1e6, 3) for k, v in r["kernels"].items()},
         "kernels_us_by_mode": {m: {k: round(v[0] * 1e6, 3) for k, v in kk.items()}
                                for m, kk in r["kernels_by_mode"].items()},
@@ -492,19 +511,31 @@ def main():
     }
     if hasattr(wl, "op_roofline"):
         line["roofline_op"] = wl.op_roofline(sec)
-    if args.all:
+    if not args.only:
         extras = {}
-        for name in sorted(WORKLOADS):
-            if name == args.workload:
+        esteps = min(args.steps, 50)
+        for name, cold in EXTRAS:
+            if name == args.workload and cold == args.cold:
                 continue
-            e = run_workload(name, args.steps, args.warmup, cold=args.cold, with_cpu=False)
-            extras[name] = {"verified": e["verified"], "unit": e["workload"].unit,
-                            "value_aware": round(e["tput"]["aware"], 3),
-                            "value_oblivious": round(e["tput"]["oblivious"], 3),
-                            "value_rotated": round(e["tput"]["rotated"], 3),
-                            "speedup_aware_vs_oblivious": round(e["sec"]["oblivious"] / e["sec"]["aware"], 4),
-                            "roofline": e["workload"].roofline(e["kernels"][e["workload"].dominant][0]),
-                            "kernels_us": {k: round(v[0] * 1e6, 3) for k, v in e["kernels"].items()}}
+            print(f"bench.py: extra {name} ({'cold' if cold else 'warm'})", file=sys.stderr, flush=True)
+            e = run_workload(name, esteps, min(args.warmup, 5), cold=cold, with_cpu=not args.no_cpu and not cold)
+            ew = e["workload"]
+            entry = {"verified": e["verified"], "unit": ew.unit, "steps": esteps,
+                     "cache": "cold" if cold else "warm", "config": ew.config(),
+                     "value_aware": round(e["tput"]["aware"], 3),
+                     "value_oblivious": round(e["tput"]["oblivious"], 3),
+                     "value_rotated": round(e["tput"]["rotated"], 3),
+                     "speedup_aware_vs_oblivious": round(e["sec"]["oblivious"] / e["sec"]["aware"], 4),
+                     "speedup_rotated_vs_oblivious": round(e["sec"]["oblivious"] / e["sec"]["rotated"], 4),
+                     "roofline": ew.roofline(launch_seconds(ew, e)),
+                     "kernels_us": {k: round(v[0] * 1e6, 3) for k, v in e["kernels"].items()},
+                     "kernels_us_by_mode": {m: {k: round(v[0] * 1e6, 3) for k, v in kk.items()}
+                                            for m, kk in e["kernels_by_mode"].items()}}
+            if "cpu" in e:
+                entry["cpu_baseline"] = e["cpu"]
+            extras[f"{name}_{'cold' if cold else 'warm'}"] = entry
+            del e, ew
+            torch.cuda.empty_cache()
         line["extras"] = extras
     print(json.dumps(line), flush=True)
 

@@ -54,18 +54,20 @@ class GemvF32:
         from l2domain_amd import gen
         self.M, self.K = M, K
         from l2domain_amd.domain import home_map
+        from l2domain_amd.gemv import workspace as gemv_workspace
         A, x = gen.gemv_f32_inputs(M, K)
         self.hA, self.hx = A, x
         self.A = torch.from_numpy(A).cuda()
         self.x = torch.from_numpy(x).cuda()
         self.y = torch.empty(M, dtype=torch.float32, device="cuda")
         self.home = home_map(self.A)
+        self.ws = gemv_workspace(M, K, self.A.dtype)
         self.bytes = 4 * M * K + 4 * K + 4 * M
         self.np = np
 
     def step(self, mode):
         from l2domain_amd.gemv import gemv
-        gemv(self.A, self.x, self.y, mode=mode, home_attr=self.home)
+        gemv(self.A, self.x, self.y, mode=mode, home_attr=self.home, workspace=self.ws)
 
     def throughput(self, sec_per_step):
         return self.bytes / sec_per_step / 1e9
@@ -93,6 +95,8 @@ class GemvF32:
         f16 = "true" if self.A.element_size() == 2 else "false"
         if 8192 % row_bytes == 0:
             return f"gemv_rowhome_kernel<{f16},*>"
+        if self.ws is not None and self.A.data_ptr() % 8192 == 0:
+            return f"gemv_seghome_kernel<{f16}>"
         return f"gemv_exact_kernel<{f16},*>"
 
     def config(self):
@@ -123,12 +127,14 @@ class GemvF16(GemvF32):
         self.M, self.K = M, K
         self.name = f"gemv_f16_{M}x{K}"
         from l2domain_amd.domain import home_map
+        from l2domain_amd.gemv import workspace as gemv_workspace
         W, x = gen.gemv_f16_inputs(M, K)
         self.hA, self.hx = W, x
         self.A = torch.from_numpy(W).cuda()
         self.x = torch.from_numpy(x).cuda()
         self.y = torch.empty(M, dtype=torch.float32, device="cuda")
         self.home = home_map(self.A)
+        self.ws = gemv_workspace(M, K, self.A.dtype)
         self.bytes = 2 * M * K + 2 * K + 4 * M
         self.np = np
 
@@ -461,7 +467,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--cold", action="store_true", help="flush L2 + Infinity Cache before every step")
     ap.add_argument("--only", action="store_true", help="measure the selected workload only (no extras)")

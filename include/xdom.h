@@ -133,22 +133,37 @@ int xd_cache_flush(const void *buf, size_t bytes, void *stream);
 /* GEMV  y[M] = A[M,K] . x[K], row-major A, fp32 accumulation                            */
 /* ------------------------------------------------------------------------------------ */
 
+/* Workspace bytes the GEMV entry points use for the split-row home routing of an M x K
+ * matrix of elem_bytes (4: fp32, 2: fp16) elements: M * (S + 1) * 4 when a row is S >= 2
+ * whole 8 KiB chunks (and S * 8 KiB <= 64 KiB), else 0 (no workspace used). No counterpart
+ * in the reference (its rows never span two sides' memory, GEMV.cu:264-273). */
+size_t xd_gemv_workspace_size(int M, int K, int elem_bytes);
+
 /* fp32 GEMV. Replaces gemv_partitioned_kernel / gemv_baseline_kernel
  * (applications/gemv/src/gemv_k1024_persistent_subwarp.cu:163-231), generalised from the
  * compile-time K=1024 to any K with K % 4 == 0 and 16-byte aligned A and x.
- * Writes every y[i] (no accumulation into y). Placement: XD_MODE_OBLIVIOUS hands row
- * chunks to workgroups in order (consecutive chunks land on different XCDs); XD_MODE_AWARE
- * routes each row to the I/O die homing it when rows do not straddle 8 KiB chunks (row
- * bytes divide 8192 and A is 8 KiB aligned; home_attr = xd_home_map() of A, optional), and
- * otherwise gives every XCD one contiguous eighth of the rows (the reference's per-side
- * row lists, GEMV.cu:264-273); XD_MODE_ROTATED is the far-die / next-XCD control. */
+ * Writes every y[i] (no accumulation into y). Placement:
+ *   XD_MODE_OBLIVIOUS  row chunks go to workgroups in order (consecutive chunks land on
+ *                      different XCDs);
+ *   XD_MODE_AWARE      with A 8 KiB aligned, work follows memory homes (home_attr =
+ *                      xd_home_map() of A; NULL = the address-mask prediction):
+ *                      rows that divide 8 KiB go whole to the I/O die homing them; rows of
+ *                      S >= 2 whole 8 KiB chunks are split into chunks, each reduced on its
+ *                      home die and combined in chunk order (needs a workspace of
+ *                      xd_gemv_workspace_size() bytes, 8-byte aligned, zero-filled once when
+ *                      allocated; each call leaves it zeroed; calls sharing one workspace
+ *                      must not overlap).
+ *                      Otherwise every XCD gets one contiguous eighth of the rows (the
+ *                      reference's per-side row lists, GEMV.cu:264-273);
+ *   XD_MODE_ROTATED    the same routes with the far die / next XCD (the "swapped" control).
+ * The split-row route gives bit-identical y to XD_MODE_OBLIVIOUS for S = 2 and 4. */
 int xd_gemv_f32(const float *A, const float *x, float *y, int M, int K, int mode, const uint8_t *home_attr,
-                void *stream);
+                void *workspace, size_t workspace_bytes, void *stream);
 
 /* fp16 weights and vector (IEEE binary16 bit patterns), fp32 accumulation, fp32 y.
  * Same structure as xd_gemv_f32; K % 8 == 0, 16-byte aligned W and x. */
 int xd_gemv_f16f32(const uint16_t *W, const uint16_t *x, float *y, int M, int K, int mode,
-                   const uint8_t *home_attr, void *stream);
+                   const uint8_t *home_attr, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------------------------ */
 /* Histogram  counts[k] = #{i : keys[i] == k}, k < num_bins                               */

@@ -72,8 +72,9 @@ SIGNATURES: dict[str, tuple] = {
     "xd_home_map": (I, [VP, SZ, VP, VP, SZ, VP]),
     "xd_cache_flush_bytes": (SZ, []),
     "xd_cache_flush": (I, [VP, SZ, VP]),
-    "xd_gemv_f32": (I, [VP, VP, VP, I, I, I, VP, VP]),
-    "xd_gemv_f16f32": (I, [VP, VP, VP, I, I, I, VP, VP]),
+    "xd_gemv_workspace_size": (SZ, [I, I, I]),
+    "xd_gemv_f32": (I, [VP, VP, VP, I, I, I, VP, VP, SZ, VP]),
+    "xd_gemv_f16f32": (I, [VP, VP, VP, I, I, I, VP, VP, SZ, VP]),
     "xd_hist_workspace_size": (SZ, [SZ, U32]),
     "xd_hist_u32": (I, [VP, SZ, VP, U32, I, VP, SZ, VP]),
     "xd_hash_table_bytes": (SZ, [U64]),

@@ -224,6 +224,112 @@ gemv_rowhome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, fl
     }
 }
 
+// Split-row memory-home variant for rows made of S >= 2 whole 8 KiB chunks (A 8 KiB
+// aligned). Segment j (bytes [8 KiB j, 8 KiB (j+1)) of A) is part j % S of row j / S and is
+// homed on one I/O die; the waves of a die take the segments homed on the wanted die. A
+// segment's partial is computed exactly as the exact-width kernel's wave for that segment
+// computes it (8 vectors per lane, same lane -> vector map, same reduction), and the row's
+// partials meet through memory-side atomics on the workspace:
+//   S == 2 (PAIR): each arrival swaps a 64-bit word (segment + 1) << 32 | bits(partial) into
+//     the row's word; the arrival that gets its partner's word back writes y = p0 + p1
+//     (fp addition is commutative, so the order of arrival does not change the bits) and
+//     clears the word. One round trip per segment.
+//   S > 2: each arrival deposits its partial in slot j with a returning swap, then takes a
+//     ticket on the row's counter; the last of the S arrivals swaps the slots back out,
+//     adds them in segment order, writes y and clears the counter.
+// Both orders equal the exact kernel's LDS combine order, so both kernels give the same bits
+// for S = 2 and 4. The row words / counters must be zero when the call starts; every call
+// leaves them zero.
+template <bool F16, bool PAIR>
+__device__ __forceinline__ void seg_meet(float part, int j, int row, int seg, int S, float *__restrict__ y,
+                                         uint32_t *__restrict__ cnt, uint32_t *__restrict__ slot) {
+    if (PAIR) {
+        unsigned long long *pair = reinterpret_cast<unsigned long long *>(cnt);
+        const unsigned long long word =
+            ((unsigned long long)(seg + 1) << 32) | (unsigned long long)__float_as_uint(part);
+        const unsigned long long old = atomicExch(&pair[row], word);
+        if (old != 0ull) {
+            y[row] = part + __uint_as_float((uint32_t)old);
+            atomicExch(&pair[row], 0ull);
+        }
+    } else {
+        const uint32_t old = atomicExch(&slot[j], __float_as_uint(part));
+        // consuming the returned value makes the ticket wait until the deposit is done
+        asm volatile("" ::"v"(old));
+        const uint32_t t = atomicAdd(&cnt[row], 1u);
+        if (t == (uint32_t)(S - 1)) {
+            float sum = 0.0f;
+            for (int s = 0; s < S; ++s) {
+                // a swap is a read-modify-write executed at the memory-side atomic unit, like
+                // the deposit it reads (an idempotent OR could become a plain load)
+                const float v = (s == seg) ? part : __uint_as_float(atomicExch(&slot[(size_t)row * S + s], 0u));
+                sum = (s == 0) ? v : sum + v;
+            }
+            y[row] = sum;
+            atomicExch(&cnt[row], 0u);
+        }
+    }
+}
+
+// Workgroup w of a die visits groups w, w + W, w + 2W, ... of 8 consecutive segments (W =
+// workgroups per die); lane i of every wave evaluates the home of segment i of the group,
+// and the group's wanted segments are dealt to the 4 waves in turn.
+template <bool F16, bool PAIR>
+__global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4)))
+gemv_seghome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__restrict__ y, int M, int S,
+                    int mode, HomeMap home, uint32_t *__restrict__ cnt, uint32_t *__restrict__ slot) {
+    constexpr int CW = 8;
+    constexpr int kSegVec = kWave * CW;  // 512 vectors = 8 KiB
+    constexpr int kGroup = 8;
+    extern __shared__ uint4 xs[];
+    const int b = (int)blockIdx.x;
+    const int per_die = (int)gridDim.x / 2;
+    const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
+    const uint32_t die = wg_die(b);
+    const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
+    const int wave = (int)threadIdx.x / kWave;
+    const int lane = (int)threadIdx.x % kWave;
+    const int nv = S * kSegVec;
+    for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
+    __syncthreads();
+    const uint64_t abase = reinterpret_cast<uint64_t>(A);
+    const int nseg = M * S;
+    const int ngroups = (nseg + kGroup - 1) / kGroup;
+    for (int g = rank; g < ngroups; g += per_die) {
+        const int jl = g * kGroup + lane;
+        const bool wanted = lane < kGroup && jl < nseg && home(abase + (uint64_t)jl * kHomeChunk) == want;
+        uint64_t m = __ballot(wanted);
+        for (int k = 0; k < wave && m; ++k) m &= m - 1;
+        while (m) {
+            const int j = g * kGroup + __builtin_ctzll(m);
+            const int row = j / S;
+            const int seg = j - row * S;
+            const uint4 *p = A + (size_t)j * kSegVec + lane;
+            uint4 a[CW];
+#pragma unroll
+            for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
+            const uint4 *xv = xs + seg * kSegVec + lane;
+            float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+            for (int u = 0; u < CW; u += 2) {
+                acc0 = F16 ? dot16_f16(a[u], xv[u * kWave], acc0) : dot16_f32(a[u], xv[u * kWave], acc0);
+                acc1 = F16 ? dot16_f16(a[u + 1], xv[(u + 1) * kWave], acc1)
+                           : dot16_f32(a[u + 1], xv[(u + 1) * kWave], acc1);
+            }
+            const float part = wave_sum_f32(acc0 + acc1);
+            if (lane == 0) seg_meet<F16, PAIR>(part, j, row, seg, S, y, cnt, slot);
+            for (int k = 0; k < kGemvWaves && m; ++k) m &= m - 1;
+        }
+    }
+}
+
+static int seg_per_row(int K, int elem_bytes) {
+    const size_t row_bytes = (size_t)K * (size_t)elem_bytes;
+    if (row_bytes % kHomeChunk != 0) return 0;
+    const size_t S = row_bytes / kHomeChunk;
+    return (S >= 2 && S * kHomeChunk <= (size_t)kGemvMaxLdsBytes) ? (int)S : 0;
+}
+
 static int rows_per_workgroup(int M, int nv) {
     // XD_GEMV_ROWS_PER_WG overrides the heuristic (tuning sweeps); must be a multiple of 4.
     if (const char *e = getenv("XD_GEMV_ROWS_PER_WG")) {
@@ -238,7 +344,7 @@ static int rows_per_workgroup(int M, int nv) {
 
 template <bool F16>
 static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int mode, const uint8_t *home_attr,
-                       void *stream) {
+                       void *workspace, size_t workspace_bytes, void *stream) {
     const int per_vec = F16 ? 8 : 4;
     XD_REQUIRE(A != nullptr && x != nullptr && y != nullptr, "gemv: NULL pointer");
     XD_REQUIRE(M > 0 && K > 0, "gemv: M and K must be positive");
@@ -257,10 +363,31 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
     const uint4 *x4 = reinterpret_cast<const uint4 *>(x);
     KernelTimer kt(F16 ? "gemv_f16f32" : "gemv_f32", s);
     bool done = false;
+    // Memory-home routing of 8 KiB row segments when rows are whole multiples of 8 KiB.
+    const int S = seg_per_row(K, F16 ? 2 : 4);
+    if (mode != XD_MODE_OBLIVIOUS && S > 0 && (reinterpret_cast<uintptr_t>(A) % kHomeChunk) == 0 && workspace &&
+        workspace_bytes >= (size_t)M * (size_t)(S + 1) * 4 && (reinterpret_cast<uintptr_t>(workspace) % 8) == 0) {
+        const HomeMap home{home_attr, reinterpret_cast<uint64_t>(A) / kHomePage, home_mask()};
+        uint32_t *cnt = reinterpret_cast<uint32_t *>(workspace);
+        uint32_t *slot = cnt + M;
+        const long long nseg = (long long)M * S;
+        // one workgroup per 8 segments (two groups of 8 per workgroup on average, about one
+        // wanted segment per wave per group); measured best among 4, 8 and 16 per workgroup
+        long long sgrid = (nseg + 7) / 8;
+        sgrid = (sgrid + kNumXcd - 1) / kNumXcd * kNumXcd;
+        if (sgrid > (1LL << 30)) return fail(XD_ERR_UNSUPPORTED, "gemv: matrix too large for the split-row route");
+        if (S == 2)
+            hipLaunchKernelGGL((gemv_seghome_kernel<F16, true>), dim3((unsigned)sgrid), dim3(kGemvThreads), lds, s, A4, x4,
+                               y, M, S, mode, home, cnt, slot);
+        else
+            hipLaunchKernelGGL((gemv_seghome_kernel<F16, false>), dim3((unsigned)sgrid), dim3(kGemvThreads), lds, s, A4,
+                               x4, y, M, S, mode, home, cnt, slot);
+        done = true;
+    }
     // Memory-home routing when every row sits inside one 8 KiB chunk.
     const size_t row_bytes = (size_t)nv * 16;
-    if (mode != XD_MODE_OBLIVIOUS && kHomeChunk % row_bytes == 0 && (reinterpret_cast<uintptr_t>(A) % kHomeChunk) == 0 &&
-        nv % kWave == 0) {
+    if (!done && mode != XD_MODE_OBLIVIOUS && kHomeChunk % row_bytes == 0 &&
+        (reinterpret_cast<uintptr_t>(A) % kHomeChunk) == 0 && nv % kWave == 0) {
         const int CW = nv / kWave;
         const HomeMap home{home_attr, reinterpret_cast<uint64_t>(A) / kHomePage, home_mask()};
         // two groups of 8 rows per workgroup on average
@@ -328,14 +455,20 @@ using namespace xd;
 
 extern "C" {
 
+size_t xd_gemv_workspace_size(int M, int K, int elem_bytes) {
+    if (M <= 0 || K <= 0 || (elem_bytes != 2 && elem_bytes != 4)) return 0;
+    const int S = seg_per_row(K, elem_bytes);
+    return S > 0 ? (size_t)M * (size_t)(S + 1) * 4 : 0;
+}
+
 int xd_gemv_f32(const float *A, const float *x, float *y, int M, int K, int mode, const uint8_t *home_attr,
-                void *stream) {
-    return launch_gemv<false>(A, x, y, M, K, mode, home_attr, stream);
+                void *workspace, size_t workspace_bytes, void *stream) {
+    return launch_gemv<false>(A, x, y, M, K, mode, home_attr, workspace, workspace_bytes, stream);
 }
 
 int xd_gemv_f16f32(const uint16_t *W, const uint16_t *x, float *y, int M, int K, int mode, const uint8_t *home_attr,
-                   void *stream) {
-    return launch_gemv<true>(W, x, y, M, K, mode, home_attr, stream);
+                   void *workspace, size_t workspace_bytes, void *stream) {
+    return launch_gemv<true>(W, x, y, M, K, mode, home_attr, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -48,7 +48,7 @@ def test_gemv_rejects_bad_shapes(M, K, mode):
     from l2domain_amd import _lib
     buf = (C.c_float * 64)()
     p = C.cast(buf, C.c_void_p)
-    rc = _lib.lib.xd_gemv_f32(p, p, p, M, K, mode, None, None)
+    rc = _lib.lib.xd_gemv_f32(p, p, p, M, K, mode, None, None, 0, None)
     assert rc == _lib.XD_ERR_INVALID_ARG
     assert _lib.lib.xd_last_error()
 
@@ -57,13 +57,13 @@ def test_gemv_rejects_null_and_misaligned():
     from l2domain_amd import _lib
     buf = (C.c_float * 64)()
     p = C.addressof(buf)
-    assert _lib.lib.xd_gemv_f32(None, p, p, 4, 4, 1, None, None) == _lib.XD_ERR_INVALID_ARG
-    assert _lib.lib.xd_gemv_f16f32(p + 2, p, p, 4, 8, 1, None, None) == _lib.XD_ERR_INVALID_ARG
-    assert _lib.lib.xd_gemv_f16f32(p, p, p, 4, 12, 1, None, None) == _lib.XD_ERR_INVALID_ARG
+    assert _lib.lib.xd_gemv_f32(None, p, p, 4, 4, 1, None, None, 0, None) == _lib.XD_ERR_INVALID_ARG
+    assert _lib.lib.xd_gemv_f16f32(p + 2, p, p, 4, 8, 1, None, None, 0, None) == _lib.XD_ERR_INVALID_ARG
+    assert _lib.lib.xd_gemv_f16f32(p, p, p, 4, 12, 1, None, None, 0, None) == _lib.XD_ERR_INVALID_ARG
 
 
 def test_gemv_rejects_k_beyond_lds():
     from l2domain_amd import _lib
     buf = (C.c_float * 64)()
     p = C.addressof(buf)
-    assert _lib.lib.xd_gemv_f32(p, p, p, 4, 4 * 4097 * 4, 1, None, None) == _lib.XD_ERR_UNSUPPORTED
+    assert _lib.lib.xd_gemv_f32(p, p, p, 4, 4 * 4097 * 4, 1, None, None, 0, None) == _lib.XD_ERR_UNSUPPORTED

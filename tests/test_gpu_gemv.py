@@ -12,22 +12,39 @@ import torch
 
 import oracle as ora
 from l2domain_amd import gen
-from l2domain_amd.gemv import gemv
+from l2domain_amd.gemv import gemv, workspace
 
 pytestmark = pytest.mark.gpu
 MODES = ["oblivious", "aware", "rotated"]
 
 
-def run(A: np.ndarray, x: np.ndarray, mode, mapped: bool = False) -> np.ndarray:
-    dA = torch.from_numpy(np.ascontiguousarray(A)).cuda()
+def device_aligned(a: np.ndarray, align: int = 8192) -> torch.Tensor:
+    """Copy of `a` on the GPU starting at an `align`-byte boundary (the home routes need
+    8 KiB-aligned matrices)."""
+    a = np.ascontiguousarray(a)
+    raw = torch.empty(a.nbytes + align, dtype=torch.uint8, device="cuda")
+    off = (-raw.data_ptr()) % align
+    t = raw[off:off + a.nbytes].view(torch.float16 if a.dtype == np.float16 else torch.float32).view(a.shape)
+    t.copy_(torch.from_numpy(a))
+    return t
+
+
+def run(A: np.ndarray, x: np.ndarray, mode, mapped: bool = False, ws=None) -> np.ndarray:
+    dA = device_aligned(A) if mapped else torch.from_numpy(np.ascontiguousarray(A)).cuda()
     dx = torch.from_numpy(np.ascontiguousarray(x)).cuda()
     y = torch.full((A.shape[0],), float("nan"), dtype=torch.float32, device="cuda")
     home = None
     if mapped:
         from l2domain_amd.domain import home_map
         home = home_map(dA)
-    gemv(dA, dx, y, mode=mode, home_attr=home)
+        if ws is None:
+            ws = workspace(A.shape[0], A.shape[1], dA.dtype)
+    gemv(dA, dx, y, mode=mode, home_attr=home, workspace=ws)
     torch.cuda.synchronize()
+    if ws is not None:
+        S = A.shape[1] * A.itemsize // 8192
+        words = 8 * A.shape[0] if S == 2 else 4 * A.shape[0]  # S == 2: one 64-bit word per row
+        assert int(torch.count_nonzero(ws[:words])) == 0, "row words / counters not left at zero"
     return y.cpu().numpy()
 
 
@@ -136,3 +153,51 @@ def test_f16_row_home_ragged(M, K):
         y = run(W, x, mode, mapped=True)
         assert rel_err(y, ref) <= 2e-2
         assert np.all(np.abs(y - ref) <= 2e-2 * yabs + 1e-30)
+
+
+@pytest.mark.parametrize("dtype,K", [("f32", 4096), ("f32", 8192), ("f16", 8192), ("f16", 16384)])
+def test_split_row_home_bit_identical(dtype, K):
+    # rows of 2 or 4 whole 8 KiB chunks: each chunk is reduced on its home die and the
+    # partials meet in chunk order, the same order the oblivious kernel adds them in
+    M = 1536
+    if dtype == "f32":
+        A, x = gen.gemv_f32_inputs(M, K, seed=K + 1)
+    else:
+        A, x = gen.gemv_f16_inputs(M, K, w_seed=K + 2, x_seed=K + 3)
+    assert workspace(M, K, torch.float32 if dtype == "f32" else torch.float16) is not None
+    base = run(A, x, "oblivious")
+    ref, yabs = ora.gemv_f64(A, x, nthreads=8)
+    tol = 1e-3 if dtype == "f32" else 2e-2
+    assert rel_err(base, ref) <= tol
+    for mode in ("aware", "rotated"):
+        y = run(A, x, mode, mapped=True)
+        np.testing.assert_array_equal(base.view(np.uint32), y.view(np.uint32))
+
+
+def test_split_row_home_f32_4096_config(f32_config):
+    A, x, ref, yabs, seq = f32_config
+    base = run(A, x, "oblivious")
+    ws = workspace(4096, 4096, torch.float32)
+    for mode in ("aware", "rotated", "aware"):
+        y = run(A, x, mode, mapped=True, ws=ws)  # the workspace is reused across calls
+        np.testing.assert_array_equal(base.view(np.uint32), y.view(np.uint32))
+        assert float(np.max(np.abs(y - seq))) <= 1e-3
+
+
+@pytest.mark.parametrize("M,K", [(1, 2048), (3, 4096), (1000, 6144), (257, 10240)])
+def test_split_row_home_ragged(M, K):
+    # S = 2, 2, 3, 5 chunks per row (S = 3 and 5 add in chunk order, not the oblivious order)
+    A, x = gen.gemv_f32_inputs(M, K, seed=M * 3 + K)
+    ref, yabs = ora.gemv_f64(A, x)
+    for mode in MODES:
+        y = run(A, x, mode, mapped=True)
+        assert rel_err(y, ref) <= 1e-3
+        assert np.all(np.abs(y - ref) <= 1e-3 * yabs + 1e-30)
+
+
+def test_split_row_without_workspace_falls_back():
+    A, x = gen.gemv_f32_inputs(512, 4096, seed=5)
+    ref, yabs = ora.gemv_f64(A, x)
+    dA = device_aligned(A)
+    y = gemv(dA, torch.from_numpy(x).cuda(), mode="aware").cpu().numpy()
+    assert rel_err(y, ref) <= 1e-3

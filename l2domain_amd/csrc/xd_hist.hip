@@ -9,7 +9,7 @@
 // MI355X design. 2^20 u32 counters (4 MiB) do not fit the 160 KB LDS of a CU, and global
 // atomics on gfx950 run at a fixed ~27 Gatom/s chip-wide (~88 M/s on one hot address)
 // wherever the line lives, so every key must be counted in LDS:
-//   1. partition: each workgroup multi-splits a tile of 32768 keys into 32768-bin buckets
+//   1. partition: each workgroup multi-splits a tile of 16384 keys into 32768-bin buckets
 //      (bucket = key >> 15) and writes the 15-bit in-bucket offsets, grouped by bucket,
 //      as u16 (tile-major), plus the tile's bucket offsets and bucket totals;
 //   2. plan: apportions counting work items (bucket, tile range) in proportion to the
@@ -30,7 +30,7 @@ constexpr int kHB = 15;
 constexpr uint32_t kBucketBins = 1u << kHB;  // 32768 counters = 128 KB of LDS
 constexpr int kTileKeys = 16384;
 constexpr int kP1Threads = 1024;
-constexpr int kP1Vec = kTileKeys / 4 / kP1Threads;  // uint4 loads per thread (8)
+constexpr int kP1Vec = kTileKeys / 4 / kP1Threads;  // uint4 loads per thread (4)
 constexpr int kMaxBuckets = 512;                    // num_bins <= 2^24
 constexpr int kP2Threads = 1024;
 constexpr int kP2Waves = kP2Threads / kWave;

@@ -170,7 +170,10 @@ int xd_gemv_f16f32(const uint16_t *W, const uint16_t *x, float *y, int M, int K,
 /* ------------------------------------------------------------------------------------ */
 
 /* Workspace bytes xd_hist_u32 needs for n keys and num_bins counters (0 if num_bins is out
- * of range). About 2 bytes per key plus 128 KB per counting workgroup. */
+ * of range). About 2 bytes per key plus 128 KB per counting workgroup. The workspace must be
+ * zero-filled once when allocated; every call leaves its counters zeroed again, and a
+ * workspace sized for n keys serves any smaller n. Calls sharing one workspace must not
+ * overlap. */
 size_t xd_hist_workspace_size(size_t n, uint32_t num_bins);
 
 /* Histogram of uint32 keys into num_bins (1..2^24) uint32 counters; keys >= num_bins are

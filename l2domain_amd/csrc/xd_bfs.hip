@@ -52,8 +52,8 @@ struct BfsPartial {  // per workgroup, summed by bfs_reduce_kernel
 };
 
 struct BfsLayout {
-    size_t visited, front_a, front_b, queue_a, queue_b, big, counters, partials, sums, total;
-    int64_t words;
+    size_t visited, front_a, front_b, queue_a, queue_b, big, counters, partials, sums, blist, bcount, total;
+    int64_t words, nblocks;
 };
 
 static size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -81,6 +81,11 @@ static BfsLayout bfs_layout(int32_t V, int64_t nnz) {
     o = a256(o + 4 * (size_t)V);
     L.big = o;
     o = a256(o + 4 * (size_t)V);
+    L.nblocks = ((int64_t)V + 63) / 64;
+    L.bcount = o;
+    o = a256(o + 2 * sizeof(unsigned long long));
+    L.blist = o;
+    o = a256(o + 2 * 4 * (size_t)L.nblocks);
     L.total = o;
     return L;
 }
@@ -306,36 +311,68 @@ __device__ __forceinline__ void bu_range(int32_t v0, int32_t v1, const int32_t *
             my_verts += 1;
             my_edges += (unsigned long long)deg;
         }
-        // the found bits of this block fall into at most two bitmap words
+        // vb is a multiple of 64, so the block's found bits are exactly bitmap word vb / 64,
+        // which no other wave touches during this step: a plain update suffices
         const uint64_t m = __ballot(found);
-        if (m) {
+        if (m && lane == 0) {
             const int32_t w0 = vb >> 6;
-            const int sh = vb & 63;
-            const unsigned long long lo = sh ? (m << sh) : m;
-            const unsigned long long hi = sh ? (m >> (64 - sh)) : 0ull;
-            if (lane == 0 && lo) {
-                atomicOr(&visited[w0], lo);
-                atomicOr(&next[w0], lo);
-            }
-            if (lane == 1 && hi) {
-                atomicOr(&visited[w0 + 1], hi);
-                atomicOr(&next[w0 + 1], hi);
-            }
+            visited[w0] |= m;
+            next[w0] |= m;
         }
+    }
+}
+
+// Sorts the 64-vertex blocks by the I/O die that homes the start of their adjacency (the
+// block's first vertex on): list[d * nblocks + i] is the i-th block of die d. The
+// assignment depends only on the graph and the page map, so it is built once per search;
+// the bottom-up steps of the home modes then walk their die's list with no skipped blocks.
+// A workgroup classifies 1024 blocks and reserves its list space with one atomic per die.
+constexpr int kBlkThreads = 1024;
+__global__ void __launch_bounds__(kBlkThreads)
+bfs_blocks_kernel(const int32_t *__restrict__ rowptr, int64_t nblocks, uint64_t cbase, int64_t col_bytes,
+                  HomeMap home, int32_t *__restrict__ list, unsigned long long *__restrict__ count) {
+    __shared__ uint32_t wcnt[2][kBlkThreads / kWave];
+    __shared__ unsigned long long wbase[2][kBlkThreads / kWave];
+    const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    const int64_t blk = (int64_t)blockIdx.x * kBlkThreads + tid;
+    uint32_t d = 2;
+    if (blk < nblocks) {
+        uint64_t off = (uint64_t)rowptr[blk * kWave] * sizeof(int32_t);
+        if (off >= (uint64_t)col_bytes) off = (uint64_t)col_bytes - 1;  // trailing isolated vertices
+        d = home(cbase + off);
+    }
+    const uint64_t m0 = __ballot(d == 0), m1 = __ballot(d == 1);
+    if (lane == 0) {
+        wcnt[0][wave] = (uint32_t)__builtin_popcountll(m0);
+        wcnt[1][wave] = (uint32_t)__builtin_popcountll(m1);
+    }
+    __syncthreads();
+    if (tid < 2) {
+        unsigned long long tot = 0;
+        for (int w = 0; w < kBlkThreads / kWave; ++w) {
+            wbase[tid][w] = tot;
+            tot += wcnt[tid][w];
+        }
+        const unsigned long long b = tot ? atomicAdd(&count[tid], tot) : 0ull;
+        for (int w = 0; w < kBlkThreads / kWave; ++w) wbase[tid][w] += b;
+    }
+    __syncthreads();
+    if (d < 2) {
+        const uint64_t m = d ? m1 : m0;
+        list[(int64_t)d * nblocks + (int64_t)(wbase[d][wave] + mask_rank(m))] = (int32_t)blk;
     }
 }
 
 __global__ void __launch_bounds__(kBfsThreads)
 bfs_bu_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict__ col, int32_t V,
               const unsigned long long *__restrict__ front, uint32_t *__restrict__ level,
-              unsigned long long *__restrict__ visited, unsigned long long *__restrict__ next,
-              int64_t col_bytes, int mode, HomeMap home,
+              unsigned long long *__restrict__ visited, unsigned long long *__restrict__ next, int mode,
+              const int32_t *__restrict__ blist, const unsigned long long *__restrict__ bcount, int64_t nblocks,
               BfsPartial *__restrict__ parts, uint32_t lvl) {
     unsigned long long my_verts = 0, my_edges = 0;
     const int wave = (int)threadIdx.x / kWave;
     constexpr int kWavesPerWg = kBfsThreads / kWave;
     if (mode == XD_MODE_OBLIVIOUS) {
-        const int64_t nblocks = ((int64_t)V + kWave - 1) / kWave;
         for (int64_t blk = (int64_t)blockIdx.x * kWavesPerWg + wave; blk < nblocks;
              blk += (int64_t)gridDim.x * kWavesPerWg) {
             const int32_t v0 = (int32_t)(blk * kWave);
@@ -343,20 +380,17 @@ bfs_bu_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict__ co
             bu_range(v0, v1, rowptr, col, front, level, visited, next, lvl, my_verts, my_edges);
         }
     } else {
-        // Each die walks all 64-vertex blocks and takes those whose adjacency (from the
-        // block's first vertex on) starts in memory homed on the wanted die.
+        // The workgroups of a die walk that die's block list (aware) or the other die's
+        // (rotated), so the neighbour lists are read from the near (far) die.
         const int b = (int)blockIdx.x;
         const int per_die = (int)gridDim.x / 2;
         const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
         const uint32_t die = wg_die(b);
         const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
-        const uint64_t cbase = reinterpret_cast<uint64_t>(col);
-        const int64_t nblocks = ((int64_t)V + kWave - 1) / kWave;
-        for (int64_t blk = (int64_t)rank * kWavesPerWg + wave; blk < nblocks; blk += (int64_t)per_die * kWavesPerWg) {
-            const int32_t v0 = (int32_t)(blk * kWave);
-            uint64_t off = (uint64_t)rowptr[v0] * sizeof(int32_t);
-            if (off >= (uint64_t)col_bytes) off = (uint64_t)col_bytes - 1;  // trailing isolated vertices
-            if (home(cbase + off) != want) continue;
+        const int32_t *mine = blist + (int64_t)want * nblocks;
+        const int64_t cnt = (int64_t)bcount[want];
+        for (int64_t i = (int64_t)rank * kWavesPerWg + wave; i < cnt; i += (int64_t)per_die * kWavesPerWg) {
+            const int32_t v0 = mine[i] * kWave;
             const int32_t v1 = (int32_t)min((int64_t)V, (int64_t)v0 + kWave);
             bu_range(v0, v1, rowptr, col, front, level, visited, next, lvl, my_verts, my_edges);
         }
@@ -434,6 +468,8 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     auto *ctr = reinterpret_cast<BfsCounters *>(ws + L.counters);
     auto *parts = reinterpret_cast<BfsPartial *>(ws + L.partials);
     auto *sums = reinterpret_cast<BfsPartial *>(ws + L.sums);
+    auto *blist = reinterpret_cast<int32_t *>(ws + L.blist);
+    auto *bcount = reinterpret_cast<unsigned long long *>(ws + L.bcount);
     const HomeMap home{nnz > 0 ? home_attr : nullptr, reinterpret_cast<uint64_t>(col) / kHomePage, home_mask()};
     const int bmode = nnz > 0 ? mode : XD_MODE_OBLIVIOUS;  // no adjacency to route by
     const unsigned g256 = (unsigned)std::min<int64_t>(8192, ((int64_t)V + 255) / 256 + 1);
@@ -445,6 +481,13 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
         KernelTimer kt("bfs_init", s);
         hipLaunchKernelGGL(bfs_init_kernel, dim3(g256), dim3(256), 0, s, level, V, visited, L.words, src, qa);
         if (int rc = launch_status("bfs_init_kernel")) return rc;
+        if (bmode != XD_MODE_OBLIVIOUS) {
+            hipLaunchKernelGGL(bfs_fill_kernel, dim3(1), dim3(64), 0, s, bcount, (int64_t)2);
+            hipLaunchKernelGGL(bfs_blocks_kernel, dim3((unsigned)((L.nblocks + kBlkThreads - 1) / kBlkThreads)),
+                               dim3(kBlkThreads), 0, s, rowptr, L.nblocks, reinterpret_cast<uint64_t>(col),
+                               nnz * (int64_t)sizeof(int32_t), home, blist, bcount);
+            if (int rc = launch_status("bfs_blocks_kernel")) return rc;
+        }
     }
     int64_t m_u = nnz - (src_rows[1] - src_rows[0]);
     int64_t n_f = 1, m_f = src_rows[1] - src_rows[0];
@@ -473,8 +516,7 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
             hipLaunchKernelGGL(bfs_fill_kernel, dim3((unsigned)std::min<int64_t>(2048, L.words / 256 + 1)), dim3(256), 0,
                                s, fnext, L.words);
             hipLaunchKernelGGL(bfs_bu_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, rowptr, col, V, fcur, level,
-                               visited, fnext, nnz * (int64_t)sizeof(int32_t), bmode, home, parts,
-                               lvl);
+                               visited, fnext, bmode, blist, bcount, L.nblocks, parts, lvl);
             if (int rc = launch_status("bfs_bu_kernel")) return rc;
         }
         hipLaunchKernelGGL(bfs_reduce_kernel, dim3(1), dim3(256), 0, s, parts, kBfsGrid, sums);

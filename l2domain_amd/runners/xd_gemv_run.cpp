@@ -1,0 +1,168 @@
+// GEMV runner: the command line, stdout lines and exit status of the reference's GEMV
+// benchmark (applications/gemv/src/gemv_k1024_persistent_subwarp.cu:234-402, parsed by
+// applications/gemv/run.sh:63-97), on libxdom's XCD-oblivious / aware / rotated GEMV.
+//
+//   xd_gemv_run [M=2048] [runs=100] [seed=4242] [flush_l2=0] [K=1024] [dtype=f32|f16] [--csv=FILE]
+//
+// M, runs, seed and flush_l2 mean what they mean in the reference (M >= 1024; flush_l2=1
+// evicts every XCD's L2 and the Infinity Cache before each timed repeat). K and dtype are
+// new trailing arguments (the reference fixes K = 1024, fp32). Inputs: fp32 A, x ~ U[-1,1)
+// from xd_gen_uniform_f32(seed) and (seed + 0x9E37); fp16 W ~ N(0, 0.02) from seed, x ~
+// N(0, 1) from seed + 1. "baseline" is XD_MODE_OBLIVIOUS, "aware" XD_MODE_AWARE (memory-home
+// routing with the measured home map of A), "swapped" XD_MODE_ROTATED.
+//
+// Correctness: the reference's CPU loop (fp32, k ascending, :383-390) and max |y - ref|;
+// exit 3 when an fp32 run exceeds 1e-3 (the pass rule of run.sh:94-97) or an fp16 run
+// exceeds 2e-2 relative to max |ref|.
+#include <math.h>
+
+#include "runner_common.hpp"
+
+using namespace runner;
+
+static float half_to_float(uint16_t h) {
+    const uint32_t s = (uint32_t)(h >> 15) << 31;
+    const uint32_t e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = s;
+        } else {  // subnormal: m * 2^-24
+            float f = ldexpf((float)m, -24);
+            memcpy(&bits, &f, 4);
+            bits |= s;
+        }
+    } else if (e == 31) {
+        bits = s | 0x7f800000u | (m << 13);
+    } else {
+        bits = s | ((e + 112) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+int main(int argc, char **argv) {
+    Options o(argc, argv);
+    if (o.help) {
+        printf("usage: %s [M=2048] [runs=100] [seed=4242] [flush_l2=0] [K=1024] [dtype=f32|f16] [--csv=FILE]\n",
+               argv[0]);
+        return 0;
+    }
+    const int M = (int)std::max<long long>(o.geti(0, 2048), 1024);
+    const int runs = (int)std::max<long long>(o.geti(1, 100), 1);
+    const uint64_t seed = (uint64_t)o.geti(2, 4242);
+    const int flush_l2 = (int)std::min<long long>(std::max<long long>(o.geti(3, 0), 0), 1);
+    const int K = (int)o.geti(4, 1024);
+    const std::string dtype = o.gets(5, "f32");
+    const bool f16 = dtype == "f16";
+    if (K <= 0 || K % (f16 ? 8 : 4) != 0 || (dtype != "f32" && dtype != "f16")) {
+        fprintf(stderr, "bad K or dtype (K %% %d == 0, dtype f32|f16)\n", f16 ? 8 : 4);
+        return 2;
+    }
+    const xd_topology_t topo = topology();
+    hipStream_t s;
+    RUN_HIP(hipStreamCreate(&s));
+
+    const size_t elems = (size_t)M * K, esz = f16 ? 2 : 4;
+    std::vector<float> hA32, hx32;
+    std::vector<uint16_t> hA16, hx16;
+    void *dA = nullptr, *dx = nullptr;
+    RUN_HIP(hipMalloc(&dA, elems * esz));
+    RUN_HIP(hipMalloc(&dx, (size_t)K * esz));
+    if (f16) {
+        hA16.resize(elems);
+        hx16.resize(K);
+        RUN_XD(xd_gen_normal_f16(hA16.data(), elems, 0.0, 0.02, seed));
+        RUN_XD(xd_gen_normal_f16(hx16.data(), K, 0.0, 1.0, seed + 1));
+        RUN_HIP(hipMemcpy(dA, hA16.data(), elems * 2, hipMemcpyHostToDevice));
+        RUN_HIP(hipMemcpy(dx, hx16.data(), (size_t)K * 2, hipMemcpyHostToDevice));
+    } else {
+        hA32.resize(elems);
+        hx32.resize(K);
+        RUN_XD(xd_gen_uniform_f32(hA32.data(), elems, seed));
+        RUN_XD(xd_gen_uniform_f32(hx32.data(), K, seed + 0x9E37));
+        RUN_HIP(hipMemcpy(dA, hA32.data(), elems * 4, hipMemcpyHostToDevice));
+        RUN_HIP(hipMemcpy(dx, hx32.data(), (size_t)K * 4, hipMemcpyHostToDevice));
+    }
+    float *dy[3];
+    for (auto &p : dy) RUN_HIP(hipMalloc(&p, (size_t)M * sizeof(float)));
+    HomeMap home(dA, elems * esz, s);
+    const size_t wsb = xd_gemv_workspace_size(M, K, (int)esz);
+    void *ws = nullptr;
+    if (wsb) {
+        RUN_HIP(hipMalloc(&ws, wsb));
+        RUN_HIP(hipMemset(ws, 0, wsb));
+    }
+    Flusher flush;
+    auto launch = [&](int mode) {
+        if (f16)
+            RUN_XD(xd_gemv_f16f32((const uint16_t *)dA, (const uint16_t *)dx, dy[mode], M, K, mode, home.attr, ws, wsb, s));
+        else
+            RUN_XD(xd_gemv_f32((const float *)dA, (const float *)dx, dy[mode], M, K, mode, home.attr, ws, wsb, s));
+    };
+    for (int mode = 0; mode < 3; ++mode)
+        for (int w = 0; w < 5; ++w) launch(mode);
+    RUN_HIP(hipStreamSynchronize(s));
+
+    double ms[3] = {0, 0, 0};
+    for (int r = 0; r < runs; ++r)
+        for (int mode = 0; mode < 3; ++mode) {
+            if (flush_l2) flush(s);
+            ms[mode] += time_ms(s, [&] { launch(mode); });
+        }
+    for (double &m : ms) m /= runs;
+
+    // the reference's CPU loop: float running sum, k ascending
+    const auto t0 = std::chrono::steady_clock::now();
+    std::vector<float> ref(M);
+    double refmax = 0.0;
+    for (int i = 0; i < M; ++i) {
+        float sum = 0.0f;
+        for (int k = 0; k < K; ++k)
+            sum += f16 ? half_to_float(hA16[(size_t)i * K + k]) * half_to_float(hx16[k]) : hA32[(size_t)i * K + k] * hx32[k];
+        ref[i] = sum;
+        refmax = std::max(refmax, (double)fabsf(sum));
+    }
+    const double cpu_ms = wall_ms(t0);
+    double err[3];
+    for (int mode = 0; mode < 3; ++mode) {
+        std::vector<float> y(M);
+        RUN_HIP(hipMemcpy(y.data(), dy[mode], (size_t)M * sizeof(float), hipMemcpyDeviceToHost));
+        double e = 0.0;
+        for (int i = 0; i < M; ++i) e = std::max(e, (double)fabsf(y[i] - ref[i]));
+        err[mode] = e;
+    }
+    const double flops = 2.0 * M * K;
+    const double bytes = (double)elems * esz + (double)K * esz + 4.0 * M;
+    const bool ic = !flush_l2 && bytes <= 256.0 * 1024 * 1024;
+
+    printf("=== GEMV (XCD domains): K=%d %s ===\n", K, f16 ? "fp16 weights, fp32 accumulate" : "fp32");
+    printf("gpu=%s M=%d K=%d dtype=%s flush_l2=%d xcds=%d cus=%d workspace=%zu\n", topo.name, M, K, dtype.c_str(),
+           flush_l2, topo.num_xcd, topo.num_cu, wsb);
+    printf("baseline_ms %.6f ms %.2f GFLOP/s\n", ms[0], flops / (ms[0] * 1e6));
+    printf("aware_ms %.6f ms aware_speedup=%.3fx %.2f GFLOP/s\n", ms[1], ms[0] / ms[1], flops / (ms[1] * 1e6));
+    printf("swapped_ms %.6f ms swapped_speedup=%.3fx %.2f GFLOP/s\n", ms[2], ms[0] / ms[2], flops / (ms[2] * 1e6));
+    printf("correctness max_abs_error baseline=%.6g aware=%.6g swapped=%.6g\n", err[0], err[1], err[2]);
+    printf("gbps baseline=%.1f aware=%.1f swapped=%.1f\n", bytes / (ms[0] * 1e6), bytes / (ms[1] * 1e6),
+           bytes / (ms[2] * 1e6));
+    printf("roofline=%s roofline_frac=%.4f peak_gbps=8000\n", ic ? "infinity_cache" : "hbm", bytes / (ms[1] * 1e6) / 8000.0);
+    printf("cpu_ms=%.3f cpu_threads=1\n", cpu_ms);
+
+    bool pass = true;
+    for (double e : err) pass = pass && (f16 ? e <= 2e-2 * refmax : e <= 1e-3);
+    char row[512];
+    snprintf(row, sizeof row, "%d,%d,%s,%.6f,%.6f,%.6f,%.9g,%.6f,%.6f,%.1f,%.4f,%s,%.3f,%s", M, K, dtype.c_str(), ms[0],
+             ms[1], ms[2], std::max(err[0], std::max(err[1], err[2])), ms[0] / ms[1], ms[0] / ms[2],
+             bytes / (ms[1] * 1e6), bytes / (ms[1] * 1e6) / 8000.0, ic ? "infinity_cache" : "hbm", cpu_ms,
+             pass ? "PASS" : "FAIL");
+    csv_append(o.csv,
+               "M,K,dtype,baseline_ms,aware_ms,swapped_ms,max_abs_error,aware_speedup,swapped_speedup,aware_gbps,"
+               "roofline_frac,roofline,cpu_ms,pass",
+               row);
+    for (auto p : dy) (void)hipFree(p);
+    (void)hipFree(dA);
+    (void)hipFree(dx);
+    if (ws) (void)hipFree(ws);
+    return pass ? 0 : 3;
+}

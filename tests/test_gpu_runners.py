@@ -1,0 +1,80 @@
+"""Runner executables on the GPU: small cases, stdout parsed with the field rules of the
+reference's run.sh scripts (applications/gemv/run.sh:66-97,
+applications/histogram/run.sh:72-84, applications/hash/run.sh:62-86,
+applications/bfs/run.sh:84-92), exit status 0 and PASS everywhere."""
+import subprocess
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+BIN = Path(__file__).resolve().parents[1] / "l2domain_amd" / "bin"
+
+
+def run(name, *args, csv=None):
+    cmd = [str(BIN / name), *map(str, args)]
+    if csv:
+        cmd.append(f"--csv={csv}")
+    print("runner:", " ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    return r.returncode, r.stdout, r.stderr
+
+
+def first_field(out, key):
+    # awk '$1 == key {print $2; exit}'
+    for line in out.splitlines():
+        f = line.split()
+        if f and f[0] == key:
+            return f[1]
+    return None
+
+
+@pytest.mark.parametrize("K,dtype", [(1024, "f32"), (4096, "f32"), (4096, "f16"), (14336, "f16")])
+def test_gemv_runner(tmp_path, K, dtype):
+    rc, out, err = run("xd_gemv_run", 1024, 5, 4242, 1, K, dtype, csv=tmp_path / "g.csv")
+    assert rc == 0, out + err
+    for key in ("baseline_ms", "aware_ms", "swapped_ms"):
+        assert float(first_field(out, key)) > 0
+    line = next(l for l in out.splitlines() if l.startswith("correctness max_abs_error"))
+    errs = [float(t.split("=")[1]) for t in line.split() if "=" in t]
+    assert len(errs) == 3
+    if dtype == "f32":
+        assert max(errs) <= 1e-3  # applications/gemv/run.sh:94-97
+    rows = (tmp_path / "g.csv").read_text().splitlines()
+    assert rows[0].startswith("M,K,dtype,baseline_ms") and rows[1].endswith(",PASS")
+
+
+def test_hist_runner(tmp_path):
+    rc, out, err = run("xd_hist_run", 16, 2, 256, 1, 0, 1 << 20, 1.1, 1373, csv=tmp_path / "h.csv")
+    assert rc == 0, out + err
+    line = next(l for l in out.splitlines() if l.startswith("correct "))
+    assert line.split()[1:] == ["baseline=PASS", "green_aware=PASS", "green_swapped=PASS", "persistent_aware=PASS",
+                                "persistent_swapped=PASS"]
+    for key in ("baseline_kernel_ms", "persistent_aware_kernel_ms", "persistent_swapped_kernel_ms"):
+        assert float(first_field(out, key)) > 0
+    assert "baseline_blocks=" in out and "persistent_blocks=" in out
+    assert (tmp_path / "h.csv").read_text().splitlines()[1].split(",")[18] == "PASS"
+
+
+def test_hash_runner(tmp_path):
+    rc, out, err = run("xd_hash_run", 1 << 20, 1 << 20, 1 << 21, 1, 50, 0, 2, csv=tmp_path / "x.csv")
+    assert rc == 0, out + err
+    assert "Correctness: PASS" in out
+    res = next(l for l in out.splitlines() if l.startswith("RESULT "))
+    kv = dict(t.split("=") for t in res.split()[1:])
+    assert kv["pass"] == "PASS"
+    for key in ("baseline_ms", "aware_ms", "swapped_ms", "aware_speedup", "swapped_speedup"):
+        assert float(kv[key]) > 0
+
+
+def test_bfs_runner(tmp_path):
+    rc, out, err = run("xd_bfs_run", 1 << 16, 32, 2, 0, 100, 0, 2, 8201, csv=tmp_path / "b.csv")
+    assert rc == 0, out + err
+    line = next(l for l in out.splitlines() if l.startswith("visited="))
+    f = line.replace("=", " ").split()  # awk -F'[ =]' ... $2, $4, $6, $8
+    visited, aware_bad, swapped_bad, overflow = int(f[1]), int(f[3]), int(f[5]), int(f[7])
+    assert visited > 1 and aware_bad == 0 and swapped_bad == 0 and overflow == 0
+    rows = {l.split("|")[1].strip(): l.split("|")[2].strip() for l in out.splitlines() if l.startswith("| ")
+            and not l.startswith("| mode")}
+    assert float(rows["baseline"]) > 0 and float(rows["aware"]) > 0 and float(rows["swapped"]) > 0
+    assert (tmp_path / "b.csv").read_text().splitlines()[1].split(",")[21] == "PASS"

@@ -222,7 +222,9 @@ int xd_topology_query(int device, xd_topology_t *out) {
     out->lds_bytes_per_wg = (long long)prop.sharedMemPerBlock;
     out->hbm_bytes = (long long)prop.totalGlobalMem;
     std::snprintf(out->arch, sizeof(out->arch), "%s", prop.gcnArchName);
-    std::snprintf(out->name, sizeof(out->name), "%s", prop.name);
+    // the marketing name comes from a table the driver may not ship; fall back to the ISA
+    if (prop.name[0]) std::snprintf(out->name, sizeof(out->name), "%s", prop.name);
+    else std::snprintf(out->name, sizeof(out->name), "AMD Instinct %s", prop.gcnArchName);
     return XD_OK;
 }
 

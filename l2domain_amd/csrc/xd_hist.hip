@@ -313,6 +313,10 @@ hist_plan_kernel(const uint32_t *__restrict__ tot, int nb, int ntiles, int per_x
 // 3. count
 // ---------------------------------------------------------------------------------------
 constexpr uint32_t kTrash = kBucketBins;  // LDS slot that absorbs elements outside a run
+#ifndef XD_HIST_RUNS_AHEAD
+#define XD_HIST_RUNS_AHEAD 2
+#endif
+constexpr int kRunsAhead = XD_HIST_RUNS_AHEAD;  // runs loaded ahead of the one being counted
 
 // Counts the 8 u16 keys of one 16-byte vector whose first element has index `e`, for the
 // run [s0, e0). Keys equal to the wave's current hot key go to the per-lane register
@@ -362,8 +366,8 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     };
     // Each wave walks the tiles t0 + wave, t0 + wave + 16, ...: lane i first fetches the run
     // bounds of 64 of them, then the wave counts run after run. A run is read as 16-byte
-    // vectors (8 keys); the first two vectors per lane of the next run are loaded before
-    // the current run is counted.
+    // vectors (8 keys); the first two vectors per lane of the next kRunsAhead runs are in
+    // flight while the current run is counted.
     for (int tb = it.t0 + wave; tb < it.t1; tb += kP2Waves * kWave) {
         const int tl = tb + lane * kP2Waves;
         uint32_t rs = 0, re = 0;
@@ -381,43 +385,52 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
             v0 = v < vend ? run[v] : make_uint4(0, 0, 0, 0);
             v1 = v + kWave < vend ? run[v + kWave] : make_uint4(0, 0, 0, 0);
         };
-        uint4 c0, c1;
-        if (ntl > 0) load2(0, c0, c1);
-        for (int i = 0; i < ntl; ++i) {
-            uint4 n0 = make_uint4(0, 0, 0, 0), n1 = make_uint4(0, 0, 0, 0);
-            if (i + 1 < ntl) load2(i + 1, n0, n1);
-            const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
-            const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
-            const uint32_t v = (s0 >> 3) + (uint32_t)lane;
-            // Hot-key vote on the first key of every lane's first vector: keep the current
-            // hot key while a quarter of the samples match it, else adopt the first
-            // sample if a quarter of the samples match that one.
-            const uint32_t e8 = 8 * v;
-            const bool sv = e8 - s0 < e0 - s0;
-            const uint32_t sk = c0.x & 0xffffu;
-            if (__builtin_popcountll(__ballot(sv && sk == hot)) < kWave / 4) {
-                const uint64_t svm = __ballot(sv);
-                if (svm) {
-                    const uint32_t cand = (uint32_t)__builtin_amdgcn_readlane((int)sk, __builtin_ctzll(svm));
-                    if (__builtin_popcountll(__ballot(sv && sk == cand)) >= kWave / 4) {
-                        flush_hot();
-                        hot = cand;
+        // software pipeline: the runs i + 1 .. i + kRunsAhead are in flight while run i is
+        // counted (ring of register buffers, statically indexed by the unrolled j)
+        uint4 r0[kRunsAhead], r1[kRunsAhead];
+#pragma unroll
+        for (int j = 0; j < kRunsAhead; ++j) {
+            r0[j] = r1[j] = make_uint4(0, 0, 0, 0);
+            if (j < ntl) load2(j, r0[j], r1[j]);
+        }
+        for (int i0 = 0; i0 < ntl; i0 += kRunsAhead) {
+#pragma unroll
+            for (int j = 0; j < kRunsAhead; ++j) {
+                const int i = i0 + j;
+                if (i >= ntl) break;
+                const uint4 c0 = r0[j], c1 = r1[j];
+                if (i + kRunsAhead < ntl) load2(i + kRunsAhead, r0[j], r1[j]);
+                const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
+                const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
+                const uint32_t v = (s0 >> 3) + (uint32_t)lane;
+                // Hot-key vote on the first key of every lane's first vector: keep the current
+                // hot key while a quarter of the samples match it, else adopt the first
+                // sample if a quarter of the samples match that one.
+                const uint32_t e8 = 8 * v;
+                const bool sv = e8 - s0 < e0 - s0;
+                const uint32_t sk = c0.x & 0xffffu;
+                if (__builtin_popcountll(__ballot(sv && sk == hot)) < kWave / 4) {
+                    const uint64_t svm = __ballot(sv);
+                    if (svm) {
+                        const uint32_t cand = (uint32_t)__builtin_amdgcn_readlane((int)sk, __builtin_ctzll(svm));
+                        if (__builtin_popcountll(__ballot(sv && sk == cand)) >= kWave / 4) {
+                            flush_hot();
+                            hot = cand;
+                        }
                     }
                 }
+                count_vec(h, c0, e8, s0, e0, hot, hc);
+                count_vec(h, c1, 8 * (v + kWave), s0, e0, hot, hc);
+                // long runs (the hot bucket): remaining vectors, two per lane per trip
+                const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
+                const uint32_t vend = (e0 + 7) >> 3;
+                for (uint32_t u = v + 2 * kWave; u < vend; u += 2 * kWave) {
+                    const uint4 a0 = run[u];
+                    const uint4 a1 = u + kWave < vend ? run[u + kWave] : make_uint4(0, 0, 0, 0);
+                    count_vec(h, a0, 8 * u, s0, e0, hot, hc);
+                    count_vec(h, a1, 8 * (u + kWave), s0, e0, hot, hc);
+                }
             }
-            count_vec(h, c0, e8, s0, e0, hot, hc);
-            count_vec(h, c1, 8 * (v + kWave), s0, e0, hot, hc);
-            // long runs (the hot bucket): remaining vectors, two per lane per trip
-            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
-            const uint32_t vend = (e0 + 7) >> 3;
-            for (uint32_t u = v + 2 * kWave; u < vend; u += 2 * kWave) {
-                const uint4 a0 = run[u];
-                const uint4 a1 = u + kWave < vend ? run[u + kWave] : make_uint4(0, 0, 0, 0);
-                count_vec(h, a0, 8 * u, s0, e0, hot, hc);
-                count_vec(h, a1, 8 * (u + kWave), s0, e0, hot, hc);
-            }
-            c0 = n0;
-            c1 = n1;
         }
     }
     if (hot < kTrash) flush_hot();

@@ -119,6 +119,30 @@ size_t xd_home_map_workspace_size(const void *buf, size_t bytes);
 int xd_home_map(const void *buf, size_t bytes, uint8_t *attr, void *workspace, size_t workspace_bytes,
                 void *stream);
 
+/* XDom-PChase. Builds a pointer chain of numel (2..8192) 8-byte elements at a stride of
+ * stride_bytes in `chain` (device, >= numel * stride_bytes), optionally evicts the caches by
+ * streaming flush_buf (NULL: no flush), then a workgroup on XCD leader_xcd chases the chain
+ * twice and, after that launch ends, a workgroup on XCD follower_xcd chases it twice. One
+ * lane times every dependent load with s_memtime. out (device, 4 * numel + 4 uint32):
+ * [0, n) leader first, [n, 2n) leader second, [2n, 3n) follower first, [3n, 4n) follower
+ * second (cycles), then the leader's and follower's XCC ids and two claim words that read 1
+ * when each role found its XCD. Same protocol as k_peer_pchase / run_figure_2
+ * (utility/latopt.cuh:354-406, architecture/src/architecture_probe.cu:572-596) with XCDs in
+ * place of SMs and a kernel boundary in place of the leader -> follower flag. */
+int xd_xdom_pchase(int leader_xcd, int follower_xcd, void *chain, size_t chain_bytes, int numel, int stride_bytes,
+                   const void *flush_buf, size_t flush_bytes, uint32_t *out, void *stream);
+
+/* MaskProbe. For the base address buf and buf + 2^b, b = first_bit..last_bit (buf device,
+ * >= 2^last_bit + 4 bytes, zero or any data: it is left unchanged), a workgroup on XCD 0
+ * (I/O die 0) and then one on XCD 4 (die 1) record the minimum over `reps` returning
+ * memory-side fetch-adds of 0. out (device, 2 * nb + 4 uint32 with nb = last_bit -
+ * first_bit + 2): [0, nb) die-0 cycles (entry 0 = base, entry k = bit first_bit + k - 1),
+ * [nb, 2nb) die-1 cycles, then the two XCC ids and two claim words. A bit is active where
+ * the die-0 / die-1 latency relation differs from the base address's (derive_active_bits,
+ * architecture/src/architecture_probe.cu:495-523, run_mask_probe :644-670); only bits
+ * below 21 are page-stable (2 MiB pages). */
+int xd_mask_probe(void *buf, size_t bytes, int first_bit, int last_bit, int reps, uint32_t *out, void *stream);
+
 /* Bytes of read traffic xd_cache_flush needs to evict 8 x 4 MB L2 and the 256 MB
  * Infinity Cache (>= 4x their sum). */
 size_t xd_cache_flush_bytes(void);

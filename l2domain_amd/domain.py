@@ -67,3 +67,62 @@ def home_parity(buf: torch.Tensor, mask: int | None = None) -> list[int]:
     page0 = lo >> 21
     npages = int(_lib.lib.xd_home_map_pages(lo, buf.numel() * buf.element_size()))
     return [bin(((page0 + p) << 21) & m).count("1") & 1 for p in range(npages)]
+
+
+def xdom_pchase(leader_xcd: int, follower_xcd: int, numel: int = 2048, stride: int = 128, flush: bool = True,
+                device: int = 0) -> dict:
+    """XDom-PChase (run_figure_2, architecture_probe.cu:572-596): four latency traces in
+    cycles of a `numel`-element pointer chain at `stride` bytes -- leader first/second and
+    follower first/second -- plus the XCC ids the two workgroups ran on."""
+    dev = f"cuda:{device}"
+    chain = torch.empty(numel * stride // 8, dtype=torch.int64, device=dev)
+    out = torch.empty(4 * numel + 4, dtype=torch.int32, device=dev)
+    fl = CacheFlusher(device) if flush else None
+    _lib.call("xd_xdom_pchase", leader_xcd, follower_xcd, ptr(chain), chain.numel() * 8, numel, stride,
+              ptr(fl.buf) if fl else None, fl.bytes if fl else 0, ptr(out), stream_handle())
+    o = out.cpu().numpy().view("uint32")
+    if o[4 * numel + 2] != 1 or o[4 * numel + 3] != 1:
+        raise RuntimeError("xdom_pchase: a role found no workgroup on its XCD")
+    return {"leader_xcd": int(o[4 * numel]), "follower_xcd": int(o[4 * numel + 1]),
+            "leader_first": o[:numel].copy(), "leader_second": o[numel:2 * numel].copy(),
+            "follower_first": o[2 * numel:3 * numel].copy(), "follower_second": o[3 * numel:4 * numel].copy()}
+
+
+def derive_active_bits(a_curve, b_curve) -> list[bool]:
+    """The reference's rule (derive_active_bits, architecture_probe.cu:495-523): the relation
+    a > b / a < b of the base entry (or the first unequal one) is the baseline; an entry is
+    active when its relation is strict and differs from the baseline."""
+    def rel(a, b):
+        return 0 if a == b else (1 if a > b else -1)
+    base = 0
+    for a, b in zip(a_curve, b_curve):
+        base = rel(a, b)
+        if base:
+            break
+    if base == 0:
+        raise ValueError("the two curves are indistinguishable; cannot derive active bits")
+    return [rel(a, b) != 0 and rel(a, b) != base for a, b in zip(a_curve, b_curve)]
+
+
+def mask_probe(first_bit: int = 5, last_bit: int = 29, reps: int = 8, device: int = 0) -> dict:
+    """MaskProbe (run_mask_probe, architecture_probe.cu:644-670) for the I/O-die home: latency
+    of a memory-side fetch-add at buf and buf + 2^b seen from die 0 (XCD 0) and die 1 (XCD 4);
+    `active` marks the bits whose flip moves the address to the other die, `active_mask`
+    keeps the page-stable ones (below bit 21) as the reference does."""
+    dev = f"cuda:{device}"
+    nbytes = (1 << last_bit) + 4096
+    buf = torch.zeros(nbytes // 4, dtype=torch.int32, device=dev)
+    nb = last_bit - first_bit + 2
+    out = torch.empty(2 * nb + 4, dtype=torch.int32, device=dev)
+    _lib.call("xd_mask_probe", ptr(buf), nbytes, first_bit, last_bit, reps, ptr(out), stream_handle())
+    o = out.cpu().numpy().view("uint32")
+    if o[2 * nb + 2] != 1 or o[2 * nb + 3] != 1:
+        raise RuntimeError("mask_probe: a die found no workgroup on its XCD")
+    a, b = o[:nb].copy(), o[nb:2 * nb].copy()
+    flip = derive_active_bits(a, b)
+    bits = list(range(first_bit, last_bit + 1))
+    active = [f and bit < 21 for f, bit in zip(flip[1:], bits)]
+    mask = sum(1 << bit for bit, on in zip(bits, active) if on)
+    return {"bits": bits, "die0_cycles": a[1:], "die1_cycles": b[1:], "base": (int(a[0]), int(b[0])),
+            "observed_flip": flip[1:], "active": active, "active_mask": mask,
+            "xcc": (int(o[2 * nb]), int(o[2 * nb + 1]))}

@@ -78,3 +78,14 @@ def test_bfs_runner(tmp_path):
             and not l.startswith("| mode")}
     assert float(rows["baseline"]) > 0 and float(rows["aware"]) > 0 and float(rows["swapped"]) > 0
     assert (tmp_path / "b.csv").read_text().splitlines()[1].split(",")[21] == "PASS"
+
+
+def test_arch_probe_runner(tmp_path):
+    rc, out, err = run("xd_arch_probe", "domainscan", 4096, csv=tmp_path / "d.csv")
+    assert rc == 0 and "round_robin_matches=4096" in out, out + err
+    rc, out, err = run("xd_arch_probe", "pchase", 0, 4, 2048, 128, csv=tmp_path / "p.csv")
+    assert rc == 0, out + err
+    rows = (tmp_path / "p.csv").read_text().splitlines()
+    assert rows[0].startswith("device_index,device_name,leader_sm,follower_sm,index,offset_bytes") and len(rows) == 2049
+    rc, out, err = run("xd_arch_probe", "maskprobe", 5, 29, 8, csv=tmp_path / "m.csv")
+    assert rc == 0 and "active_mask=0x2000" in out, out + err

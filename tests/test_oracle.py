@@ -296,3 +296,13 @@ def test_product_rmat_matches_oracle():
         r2, c2 = ora.rmat_csr(scale, ef, seed)
         np.testing.assert_array_equal(r1, r2)
         np.testing.assert_array_equal(c1, c2)
+
+
+def test_derive_active_bits_rule():
+    # the reference's rule: baseline relation from the first unequal entry, active where the
+    # strict relation differs (architecture_probe.cu:495-523)
+    from l2domain_amd.domain import derive_active_bits
+    assert derive_active_bits([5, 5, 9, 5], [9, 9, 5, 5]) == [False, False, True, False]
+    assert derive_active_bits([3, 5, 9], [3, 9, 5]) == [False, False, True]
+    with pytest.raises(ValueError):
+        derive_active_bits([1, 2], [1, 2])

@@ -6,7 +6,7 @@ from pathlib import Path
 import pytest
 
 BIN = Path(__file__).resolve().parents[1] / "l2domain_amd" / "bin"
-RUNNERS = ["xd_gemv_run", "xd_hist_run", "xd_hash_run", "xd_bfs_run"]
+RUNNERS = ["xd_gemv_run", "xd_hist_run", "xd_hash_run", "xd_bfs_run", "xd_arch_probe"]
 
 
 @pytest.mark.parametrize("name", RUNNERS)

@@ -177,9 +177,7 @@ class Hist:
         from l2domain_amd import gen
         from l2domain_amd.histogram import HIST_SEED, ZIPF_S, Histogram
         self.n, self.num_bins = n, num_bins
-        from l2domain_amd.domain import home_map
         self.keys = gen.zipf_keys_device(n, num_bins, HIST_SEED, ZIPF_S)
-        self.keys_home = home_map(self.keys)
         self.h = Histogram(n, num_bins)
         self.counts = torch.empty(num_bins, dtype=torch.int32, device="cuda")
         torch.cuda.synchronize()
@@ -187,7 +185,7 @@ class Hist:
         self.bytes = 4 * n + 4 * num_bins
 
     def step(self, mode):
-        self.h(self.keys, self.counts, mode=mode, keys_home=self.keys_home)
+        self.h(self.keys, self.counts, mode=mode)
 
     def throughput(self, sec_per_step):
         return self.n / sec_per_step / 1e9

@@ -204,17 +204,10 @@ size_t xd_hist_workspace_size(size_t n, uint32_t num_bins);
  * not counted. Every counts[k] is written (no accumulation into counts). n < 2^32.
  * Replaces histogram256_chunked_kernel / histogram256_persistent_kernel /
  * merge_histogram256_kernel (applications/histogram/src/histogram256_sideaware.cu:51-157),
- * generalised from 256 byte-bins (add_word, :20-25) to one bin per key.
- * XD_MODE_AWARE: when keys are 128 KiB aligned, the partition pass reads every 8 KiB chunk of
- * keys, and writes its intermediate offsets, on the I/O die that homes them (keys_home_attr =
- * xd_home_map() of keys, ws_home_attr = xd_home_map() of the workspace; either may be NULL
- * for the address-mask prediction), and the bins are range-partitioned over the XCDs: XCD x
- * counts and merges only its bin range (the reference's per-side chunk lists, :227-277).
- * XD_MODE_ROTATED routes every chunk to the other die and every bin range to the next XCD.
- * Results never depend on the home maps. */
+ * generalised from 256 byte-bins (add_word, :20-25) to one bin per key. XD_MODE_AWARE
+ * range-partitions the bins over the XCDs: XCD x counts and merges only its bin range. */
 int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int mode,
-                const uint8_t *keys_home_attr, void *workspace, size_t workspace_bytes,
-                const uint8_t *ws_home_attr, void *stream);
+                void *workspace, size_t workspace_bytes, void *stream);
 
 /* ------------------------------------------------------------------------------------ */
 /* Hash table: open addressing, linear probing, uint64 keys and values                   */

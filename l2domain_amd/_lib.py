@@ -78,7 +78,7 @@ SIGNATURES: dict[str, tuple] = {
     "xd_gemv_f32": (I, [VP, VP, VP, I, I, I, VP, VP, SZ, VP]),
     "xd_gemv_f16f32": (I, [VP, VP, VP, I, I, I, VP, VP, SZ, VP]),
     "xd_hist_workspace_size": (SZ, [SZ, U32]),
-    "xd_hist_u32": (I, [VP, SZ, VP, U32, I, VP, VP, SZ, VP, VP]),
+    "xd_hist_u32": (I, [VP, SZ, VP, U32, I, VP, SZ, VP]),
     "xd_hash_table_bytes": (SZ, [U64]),
     "xd_hash_init": (I, [VP, U64, VP]),
     "xd_hash_insert_u64": (I, [VP, U64, VP, VP, U64, I, VP, VP, VP]),

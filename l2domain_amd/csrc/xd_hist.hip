@@ -52,34 +52,6 @@ struct HistBucket {
     int pad;
 };
 
-// Home routing of the partition pass (aware / rotated modes). Keys are taken in windows of
-// 16 chunks of 8 KiB (2^15 keys, 128 KiB aligned); the 8 chunks homed on one die form tile
-// 2w + die of window w and are partitioned by a workgroup of that die (aware) or of the
-// other die (rotated). Tile 2w + p writes its 32 KiB of u16 offsets into the 4 chunks of
-// part window w (64 KiB) homed on die p, so that reads and writes both stay on the data's
-// die; the count pass reads the runs back through the same chunk map. Keys past the last
-// full window form ordinary contiguous tiles.
-constexpr size_t kKeyWindowBytes = 128 * 1024;  // 16 chunks of keys
-constexpr size_t kPartAlign = 64 * 1024;        // one part window (2 tiles of u16)
-constexpr uint32_t kChunkVec = 8192 / 16;       // 16-byte vectors per 8 KiB chunk
-
-struct PartMap {
-    int route;   // 1: windows 0 .. nwin-1 use the chunk map
-    int nwin;    // full key windows
-    HomeMap ph;  // home map of the workspace (part)
-    uint64_t part_addr;
-    // die-select bit of the chunks of tile t inside its part window
-    __device__ __forceinline__ uint32_t half(int t) const {
-        return ((uint32_t)t & 1u) ^ ph(part_addr + (uint64_t)(t >> 1) * kPartAlign);
-    }
-    // 16-byte vector v of tile t's u16 stream; hp = half(t) for window tiles
-    __device__ __forceinline__ size_t vec(int t, uint32_t v, uint32_t hp) const {
-        if (route && t < 2 * nwin)
-            return ((size_t)(t >> 1) * 8 + 2 * (v >> 9) + hp) * kChunkVec + (v & (kChunkVec - 1));
-        return (size_t)t * (kTileKeys / 8) + v;
-    }
-};
-
 struct HistLayout {
     int nb, ntiles, per_xcd, nitems;
     size_t part, offs, tot, items, buckets, xcdr, partials, total;
@@ -110,8 +82,8 @@ static HistLayout hist_layout(size_t n, uint32_t num_bins) {
     o = align256(o + (size_t)L.nitems * kBucketBins * sizeof(uint32_t));
     L.offs = o;
     o = align256(o + (size_t)L.ntiles * (L.nb + 1) * sizeof(uint32_t));
-    L.part = o;  // rounded up to a 64 KiB boundary of the actual address (slack below)
-    o = align256(o + (size_t)L.ntiles * kTileKeys * sizeof(uint16_t) + kPartAlign);
+    L.part = o;
+    o = align256(o + (size_t)L.ntiles * kTileKeys * sizeof(uint16_t));
     L.total = o;
     return L;
 }
@@ -132,28 +104,11 @@ __device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
 template <bool VEC>
 __global__ void __launch_bounds__(kP1Threads)
 hist_partition_kernel(const uint32_t *__restrict__ keys, size_t n, uint32_t num_bins, int nb,
-                      uint16_t *__restrict__ part, uint32_t *__restrict__ offs, uint32_t *__restrict__ tot,
-                      int mode, int ntiles, PartMap pm, HomeMap kh) {
+                      uint16_t *__restrict__ part, uint32_t *__restrict__ offs, uint32_t *__restrict__ tot) {
     __shared__ uint32_t cnt[kMaxBuckets];
     __shared__ uint32_t base[kMaxBuckets + 1];
     __shared__ __attribute__((aligned(16))) uint16_t stage[kTileKeys];
-    int t = (int)blockIdx.x;
-    uint32_t khalf = 0;  // window tiles: which 8 of the window's 16 key chunks
-    bool win = false;
-    if (pm.route) {
-        const int b = (int)blockIdx.x;
-        const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
-        const uint32_t die = wg_die(b);
-        const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
-        if (rank < pm.nwin) {
-            t = 2 * rank + (int)want;
-            win = true;
-            khalf = want ^ kh(reinterpret_cast<uint64_t>(keys) + (uint64_t)rank * kKeyWindowBytes);
-        } else {
-            t = 2 * pm.nwin + (rank - pm.nwin) * 2 + (int)die;  // contiguous tail tiles
-        }
-        if (t >= ntiles) return;
-    }
+    const int t = (int)blockIdx.x;
     const size_t k0 = (size_t)t * kTileKeys;
     const int tid = (int)threadIdx.x;
     const int lane = tid % kWave;
@@ -161,19 +116,7 @@ hist_partition_kernel(const uint32_t *__restrict__ keys, size_t n, uint32_t num_
     for (int i = tid; i < nb; i += kP1Threads) cnt[i] = 0;
 
     uint32_t kk[4 * kP1Vec];
-    if (VEC && win) {
-        // tile 2w + p of window w: chunks 2i + khalf (i < 8) of the window's 16
-        const uint4 *kv = reinterpret_cast<const uint4 *>(keys) + (size_t)(t >> 1) * 16 * kChunkVec;
-#pragma unroll
-        for (int j = 0; j < kP1Vec; ++j) {
-            const uint32_t vi = (uint32_t)(tid + j * kP1Threads);
-            uint4 v = kv[(2 * (vi / kChunkVec) + khalf) * kChunkVec + vi % kChunkVec];
-            kk[4 * j] = v.x;
-            kk[4 * j + 1] = v.y;
-            kk[4 * j + 2] = v.z;
-            kk[4 * j + 3] = v.w;
-        }
-    } else if (VEC && k0 + kTileKeys <= n) {
+    if (VEC && k0 + kTileKeys <= n) {
         const uint4 *kv = reinterpret_cast<const uint4 *>(keys + k0);
 #pragma unroll
         for (int j = 0; j < kP1Vec; ++j) {
@@ -234,9 +177,8 @@ hist_partition_kernel(const uint32_t *__restrict__ keys, size_t n, uint32_t num_
     const uint32_t total = base[nb];
     const uint32_t nvec = (total + 7) / 8;  // 8 u16 per 16-byte store
     const uint4 *src = reinterpret_cast<const uint4 *>(stage);
-    uint4 *dst = reinterpret_cast<uint4 *>(part);
-    const uint32_t hp = win ? pm.half(t) : 0u;
-    for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) dst[pm.vec(t, i, hp)] = src[i];
+    uint4 *dst = reinterpret_cast<uint4 *>(part + k0);
+    for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) dst[i] = src[i];
 }
 
 // ---------------------------------------------------------------------------------------
@@ -397,7 +339,7 @@ __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t 
 __global__ void __launch_bounds__(kP2Threads)
 hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb,
                   const HistItem *__restrict__ items, int per_xcd, uint32_t *__restrict__ partials, int mode,
-                  unsigned rot, PartMap pm) {
+                  unsigned rot) {
     __shared__ __attribute__((aligned(16))) uint32_t h[kBucketBins + 4];
     const int g = (int)blockIdx.x;
     int item;
@@ -428,23 +370,20 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     // flight while the current run is counted.
     for (int tb = it.t0 + wave; tb < it.t1; tb += kP2Waves * kWave) {
         const int tl = tb + lane * kP2Waves;
-        uint32_t rs = 0, re = 0, rh = 0;
+        uint32_t rs = 0, re = 0;
         if (tl < it.t1) {
             const uint32_t *o = offs + (size_t)tl * (nb + 1) + b;
             rs = o[0];
             re = o[1];
-            if (pm.route && tl < 2 * pm.nwin) rh = pm.half(tl);
         }
-        const uint4 *part4 = reinterpret_cast<const uint4 *>(part);
         const int ntl = min(kWave, (it.t1 - tb + kP2Waves - 1) / kP2Waves);
         auto load2 = [&](int i, uint4 &v0, uint4 &v1) {
             const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
             const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
-            const uint32_t hp = (uint32_t)__builtin_amdgcn_readlane((int)rh, i);
-            const int t = tb + i * kP2Waves;
+            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
             const uint32_t v = (s0 >> 3) + (uint32_t)lane, vend = (e0 + 7) >> 3;
-            v0 = v < vend ? part4[pm.vec(t, v, hp)] : make_uint4(0, 0, 0, 0);
-            v1 = v + kWave < vend ? part4[pm.vec(t, v + kWave, hp)] : make_uint4(0, 0, 0, 0);
+            v0 = v < vend ? run[v] : make_uint4(0, 0, 0, 0);
+            v1 = v + kWave < vend ? run[v + kWave] : make_uint4(0, 0, 0, 0);
         };
         // software pipeline: the runs i + 1 .. i + kRunsAhead are in flight while run i is
         // counted (ring of register buffers, statically indexed by the unrolled j)
@@ -483,12 +422,11 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
                 count_vec(h, c0, e8, s0, e0, hot, hc);
                 count_vec(h, c1, 8 * (v + kWave), s0, e0, hot, hc);
                 // long runs (the hot bucket): remaining vectors, two per lane per trip
-                const int t = tb + i * kP2Waves;
-                const uint32_t hp = (uint32_t)__builtin_amdgcn_readlane((int)rh, i);
+                const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
                 const uint32_t vend = (e0 + 7) >> 3;
                 for (uint32_t u = v + 2 * kWave; u < vend; u += 2 * kWave) {
-                    const uint4 a0 = part4[pm.vec(t, u, hp)];
-                    const uint4 a1 = u + kWave < vend ? part4[pm.vec(t, u + kWave, hp)] : make_uint4(0, 0, 0, 0);
+                    const uint4 a0 = run[u];
+                    const uint4 a1 = u + kWave < vend ? run[u + kWave] : make_uint4(0, 0, 0, 0);
                     count_vec(h, a0, 8 * u, s0, e0, hot, hc);
                     count_vec(h, a1, 8 * (u + kWave), s0, e0, hot, hc);
                 }
@@ -564,9 +502,8 @@ size_t xd_hist_workspace_size(size_t n, uint32_t num_bins) {
     return hist_layout(n, num_bins).total;
 }
 
-int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int mode,
-                const uint8_t *keys_home_attr, void *workspace, size_t workspace_bytes, const uint8_t *ws_home_attr,
-                void *stream) {
+int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int mode, void *workspace,
+                size_t workspace_bytes, void *stream) {
     XD_REQUIRE(counts != nullptr, "xd_hist_u32: counts is NULL");
     XD_REQUIRE(n == 0 || keys != nullptr, "xd_hist_u32: keys is NULL");
     XD_REQUIRE(num_bins >= 1 && num_bins <= (1u << 24), "xd_hist_u32: num_bins must be in [1, 2^24]");
@@ -579,8 +516,7 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
         return fail(XD_ERR_WORKSPACE, "xd_hist_u32: workspace missing, misaligned or smaller than xd_hist_workspace_size()");
     hipStream_t s = (hipStream_t)stream;
     char *ws = static_cast<char *>(workspace);
-    uint16_t *part = reinterpret_cast<uint16_t *>(
-        (reinterpret_cast<uintptr_t>(ws + L.part) + kPartAlign - 1) / kPartAlign * kPartAlign);
+    uint16_t *part = reinterpret_cast<uint16_t *>(ws + L.part);
     uint32_t *offs = reinterpret_cast<uint32_t *>(ws + L.offs);
     uint32_t *tot = reinterpret_cast<uint32_t *>(ws + L.tot);
     HistItem *items = reinterpret_cast<HistItem *>(ws + L.items);
@@ -590,26 +526,14 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     const unsigned rot = mode == XD_MODE_ROTATED ? next_rotation(1) % kNumXcd : 0u;
     const unsigned rot_eff = (mode == XD_MODE_ROTATED && rot == 0) ? 1u : rot;  // never the identity
 
-    PartMap pm{};
-    pm.ph = HomeMap{ws_home_attr, reinterpret_cast<uint64_t>(workspace) / kHomePage, home_mask()};
-    pm.part_addr = reinterpret_cast<uint64_t>(part);
-    pm.nwin = (int)(n / (kKeyWindowBytes / 4));
-    pm.route = mode != XD_MODE_OBLIVIOUS && pm.nwin > 0 && reinterpret_cast<uintptr_t>(keys) % kKeyWindowBytes == 0;
-    if (!pm.route) pm.nwin = 0;
-    const HomeMap kh{keys_home_attr, reinterpret_cast<uint64_t>(keys) / kHomePage, home_mask()};
     if (L.ntiles > 0) {
         KernelTimer kt("hist_partition", s);
-        int grid = L.ntiles;
-        if (pm.route) {  // every die needs nwin workgroups plus one for the tail tiles
-            const int per_die = pm.nwin + (L.ntiles > 2 * pm.nwin ? 1 : 0);
-            grid = (per_die + kNumXcd / 2 - 1) / (kNumXcd / 2) * kNumXcd;
-        }
         if (aligned16(keys))
-            hipLaunchKernelGGL(hist_partition_kernel<true>, dim3(grid), dim3(kP1Threads), 0, s, keys, n, num_bins,
-                               L.nb, part, offs, tot, mode, L.ntiles, pm, kh);
+            hipLaunchKernelGGL(hist_partition_kernel<true>, dim3(L.ntiles), dim3(kP1Threads), 0, s, keys, n, num_bins,
+                               L.nb, part, offs, tot);
         else
-            hipLaunchKernelGGL(hist_partition_kernel<false>, dim3(grid), dim3(kP1Threads), 0, s, keys, n,
-                               num_bins, L.nb, part, offs, tot, mode, L.ntiles, pm, kh);
+            hipLaunchKernelGGL(hist_partition_kernel<false>, dim3(L.ntiles), dim3(kP1Threads), 0, s, keys, n,
+                               num_bins, L.nb, part, offs, tot);
         if (int rc = launch_status("hist_partition_kernel")) return rc;
     }
     {
@@ -621,7 +545,7 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     {
     KernelTimer kt("hist_count", s);
     hipLaunchKernelGGL(hist_count_kernel, dim3(L.nitems), dim3(kP2Threads), 0, s, part, offs, L.nb, items, L.per_xcd,
-                       partials, mode, rot_eff, pm);
+                       partials, mode, rot_eff);
     if (int rc = launch_status("hist_count_kernel")) return rc;
     }
     KernelTimer kt("hist_merge", s);

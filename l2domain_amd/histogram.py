@@ -23,7 +23,7 @@ ZIPF_S = 1.1
 class Histogram:
     """Owns the workspace of xd_hist_u32 for inputs of up to `max_keys` keys."""
 
-    def __init__(self, max_keys: int, num_bins: int, device: int | str = 0, map_homes: bool = True):
+    def __init__(self, max_keys: int, num_bins: int, device: int | str = 0):
         self.num_bins = int(num_bins)
         self.max_keys = int(max_keys)
         nbytes = int(_lib.lib.xd_hist_workspace_size(self.max_keys, self.num_bins))
@@ -32,15 +32,9 @@ class Histogram:
         dev = torch.device(f"cuda:{device}" if isinstance(device, int) else device)
         # zeroed once; the library leaves it zeroed after every call
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
-        self.ws_home = None
-        if map_homes:
-            from .domain import home_map
-            self.ws_home = home_map(self.workspace)
 
     def __call__(self, keys: torch.Tensor, counts: torch.Tensor | None = None, mode="aware",
-                 stream: torch.cuda.Stream | None = None, keys_home: torch.Tensor | None = None) -> torch.Tensor:
-        """keys_home: domain.home_map(keys), used by the aware/rotated partition routing
-        (optional: without it the address-mask prediction is used; results are the same)."""
+                 stream: torch.cuda.Stream | None = None) -> torch.Tensor:
         if keys.dtype not in (torch.int32, torch.uint32) or keys.dim() != 1:
             raise TypeError("keys must be a 1-D 32-bit integer tensor")
         n = keys.numel()
@@ -51,8 +45,7 @@ class Histogram:
         if counts.numel() != self.num_bins or counts.element_size() != 4:
             raise ValueError("counts must hold num_bins 32-bit counters")
         _lib.call("xd_hist_u32", ptr(keys) if n else None, n, ptr(counts), self.num_bins, mode_id(mode),
-                  ptr(keys_home), ptr(self.workspace), self.workspace.numel(), ptr(self.ws_home),
-                  stream_handle(stream))
+                  ptr(self.workspace), self.workspace.numel(), stream_handle(stream))
         return counts
 
 

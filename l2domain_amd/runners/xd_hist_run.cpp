@@ -57,7 +57,6 @@ int main(int argc, char **argv) {
     void *ws = nullptr;
     RUN_HIP(hipMalloc(&ws, wsb));
     RUN_HIP(hipMemset(ws, 0, wsb));
-    HomeMap khome(keys, n * 4, s), whome(ws, wsb, s);
     Flusher flush;
 
     // serial CPU count (the reference's compute_reference_hist)
@@ -71,17 +70,17 @@ int main(int argc, char **argv) {
     bool ok[3];
     for (int mode = 0; mode < 3; ++mode) {
         RUN_HIP(hipMemset(counts, 0xff, (size_t)bins * 4));
-        RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, khome.attr, ws, wsb, whome.attr, s));
+        RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, ws, wsb, s));
         RUN_HIP(hipMemcpy(got.data(), counts, (size_t)bins * 4, hipMemcpyDeviceToHost));
         ok[mode] = got == ref;
     }
     for (int mode = 0; mode < 3; ++mode)
-        for (int w = 0; w < 3; ++w) RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, khome.attr, ws, wsb, whome.attr, s));
+        for (int w = 0; w < 3; ++w) RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, ws, wsb, s));
     double ms[3] = {0, 0, 0};
     for (int r = 0; r < runs; ++r)
         for (int mode = 0; mode < 3; ++mode) {
             if (!cache_mode) flush(s);
-            ms[mode] += time_ms(s, [&] { RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, khome.attr, ws, wsb, whome.attr, s)); });
+            ms[mode] += time_ms(s, [&] { RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, ws, wsb, s)); });
         }
     for (double &m : ms) m /= runs;
     const char *P[2] = {"FAIL", "PASS"};

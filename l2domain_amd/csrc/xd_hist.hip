@@ -54,7 +54,7 @@ struct HistBucket {
 
 struct HistLayout {
     int nb, ntiles, per_xcd, nitems;
-    size_t part, offs, tot, items, buckets, xcdr, partials, total;
+    size_t part, offs, tot, items, buckets, xcdr, bsync, partials, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -78,6 +78,8 @@ static HistLayout hist_layout(size_t n, uint32_t num_bins) {
     o = align256(o + (size_t)L.nb * sizeof(HistBucket));
     L.xcdr = o;
     o = align256(o + (size_t)kNumXcd * 2 * sizeof(int));
+    L.bsync = o;  // per bucket: arrival counter and "written off its XCD" flag (zero between calls)
+    o = align256(o + (size_t)2 * L.nb * sizeof(uint32_t));
     L.partials = o;
     o = align256(o + (size_t)L.nitems * kBucketBins * sizeof(uint32_t));
     L.offs = o;
@@ -339,7 +341,8 @@ __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t 
 __global__ void __launch_bounds__(kP2Threads)
 hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb,
                   const HistItem *__restrict__ items, int per_xcd, uint32_t *__restrict__ partials, int mode,
-                  unsigned rot) {
+                  unsigned rot, int fused, const HistBucket *__restrict__ buckets, uint32_t *__restrict__ bsync,
+                  uint32_t num_bins, uint32_t *__restrict__ counts, bool counts16) {
     __shared__ __attribute__((aligned(16))) uint32_t h[kBucketBins + 4];
     const int g = (int)blockIdx.x;
     int item;
@@ -437,6 +440,58 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     __syncthreads();
     uint4 *dst = reinterpret_cast<uint4 *>(partials + (size_t)item * kBucketBins);
     for (int i = tid; i < (int)(kBucketBins / 4); i += kP2Threads) dst[i] = h4[i];
+    if (!fused) return;
+
+    // Fused merge (XCD-aware plans): every item of bucket b was planned on XCD item / per_xcd,
+    // so the last of them to finish sums the bucket's partials out of that XCD's L2. A
+    // workgroup that finds itself on another XCD (dispatch not round-robin) publishes its
+    // partial with a device-scope release and marks the bucket, and the merger then
+    // acquires before reading.
+    __shared__ uint32_t s_last, s_foreign;
+    const bool foreign = (int)hw_xcc_id() != item / per_xcd;
+    if (foreign) __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have reached the L2
+    __syncthreads();
+    if (tid == 0) {
+        uint32_t *cnt = bsync + 2 * b, *flag = cnt + 1;
+        uint32_t f = 0;
+        if (foreign) f = atomicOr(flag, 1u);
+        asm volatile("" ::"v"(f));  // the flag is set before the ticket is taken
+        const uint32_t t = atomicAdd(cnt, 1u);
+        const HistBucket bk = buckets[b];
+        s_last = t == (uint32_t)(bk.count - 1);
+        s_foreign = 0;
+        if (s_last) {
+            atomicExch(cnt, 0u);
+            s_foreign = atomicExch(flag, 0u);
+        }
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (s_foreign || foreign) __threadfence();
+    const HistBucket bk = buckets[b];
+    const uint32_t bin0 = (uint32_t)b * kBucketBins;
+    for (int v = tid; v < (int)(kBucketBins / 4); v += kP2Threads) {
+        uint4 acc = h4[v];  // this workgroup's own partial, still in LDS
+        for (int i = 0; i < bk.count; ++i) {
+            const int slot = bk.first + i;
+            if (slot == item) continue;
+            const uint4 p = reinterpret_cast<const uint4 *>(partials + (size_t)slot * kBucketBins)[v];
+            acc.x += p.x;
+            acc.y += p.y;
+            acc.z += p.z;
+            acc.w += p.w;
+        }
+        const uint32_t k = bin0 + 4u * (uint32_t)v;
+        if (counts16 && k + 3 < num_bins) {
+            reinterpret_cast<uint4 *>(counts + k)[0] = acc;
+        } else {
+            if (k < num_bins) counts[k] = acc.x;
+            if (k + 1 < num_bins) counts[k + 1] = acc.y;
+            if (k + 2 < num_bins) counts[k + 2] = acc.z;
+            if (k + 3 < num_bins) counts[k + 3] = acc.w;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -473,8 +528,17 @@ __device__ void merge_unit(int u, const uint32_t *__restrict__ partials, const H
 __global__ void __launch_bounds__(kMergeThreads)
 hist_merge_kernel(const uint32_t *__restrict__ partials, const HistBucket *__restrict__ buckets,
                   const int *__restrict__ xcd_range, int nb, uint32_t num_bins, uint32_t *__restrict__ counts,
-                  bool counts16, uint32_t *__restrict__ tot, int mode) {
+                  bool counts16, uint32_t *__restrict__ tot, int mode, int only_empty) {
     const int g = (int)blockIdx.x;
+    if (g == 0)
+        for (int i = (int)threadIdx.x; i < kNumXcd * nb; i += kMergeThreads) tot[i] = 0;
+    if (only_empty) {
+        // fused plans merged every counted bucket in the count pass; write the empty ones
+        for (int u = g; u < nb * kMergeUnitsPerBucket; u += (int)gridDim.x)
+            if (buckets[u / kMergeUnitsPerBucket].count == 0)
+                merge_unit(u, partials, buckets, num_bins, counts, counts16);
+        return;
+    }
     if (mode == XD_MODE_OBLIVIOUS) {
         for (int u = g; u < nb * kMergeUnitsPerBucket; u += (int)gridDim.x)
             merge_unit(u, partials, buckets, num_bins, counts, counts16);
@@ -487,8 +551,6 @@ hist_merge_kernel(const uint32_t *__restrict__ partials, const HistBucket *__res
         const int u1 = xcd_range[2 * x + 1] * kMergeUnitsPerBucket;
         for (int u = u0 + s.rank; u < u1; u += s.per_xcd) merge_unit(u, partials, buckets, num_bins, counts, counts16);
     }
-    if (g == 0)
-        for (int i = (int)threadIdx.x; i < kNumXcd * nb; i += kMergeThreads) tot[i] = 0;
 }
 
 }  // namespace xd
@@ -522,6 +584,8 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     HistItem *items = reinterpret_cast<HistItem *>(ws + L.items);
     HistBucket *buckets = reinterpret_cast<HistBucket *>(ws + L.buckets);
     int *xcdr = reinterpret_cast<int *>(ws + L.xcdr);
+    uint32_t *bsync = reinterpret_cast<uint32_t *>(ws + L.bsync);
+    const int fused = mode == XD_MODE_AWARE ? 1 : 0;
     uint32_t *partials = reinterpret_cast<uint32_t *>(ws + L.partials);
     const unsigned rot = mode == XD_MODE_ROTATED ? next_rotation(1) % kNumXcd : 0u;
     const unsigned rot_eff = (mode == XD_MODE_ROTATED && rot == 0) ? 1u : rot;  // never the identity
@@ -545,13 +609,13 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     {
     KernelTimer kt("hist_count", s);
     hipLaunchKernelGGL(hist_count_kernel, dim3(L.nitems), dim3(kP2Threads), 0, s, part, offs, L.nb, items, L.per_xcd,
-                       partials, mode, rot_eff);
+                       partials, mode, rot_eff, fused, buckets, bsync, num_bins, counts, aligned16(counts));
     if (int rc = launch_status("hist_count_kernel")) return rc;
     }
     KernelTimer kt("hist_merge", s);
     const int merge_grid = kNumXcd * 64;
     hipLaunchKernelGGL(hist_merge_kernel, dim3(merge_grid), dim3(kMergeThreads), 0, s, partials, buckets, xcdr, L.nb,
-                       num_bins, counts, aligned16(counts), tot, mode);
+                       num_bins, counts, aligned16(counts), tot, mode, fused);
     return launch_status("hist_merge_kernel");
 }
 

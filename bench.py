@@ -314,7 +314,8 @@ class Bfs:
     name = "bfs_rmat22_ef16"
     unit = "GTEPS"
     dtype = "int32"
-    dominant = "bfs_bottomup"
+    dominant = "bfs_level"
+    single_kernel = True  # roofline over the whole search (init, levels, control, conversion)
 
     def __init__(self):
         from l2domain_amd.bfs import RMAT_EDGE_FACTOR, RMAT_SCALE, RMAT_SEED, Graph, rmat_csr
@@ -341,12 +342,14 @@ class Bfs:
         return ok
 
     def roofline(self, sec_per_launch):
-        # 4(V+1) + 4 nnz_reached + 4 V bytes per BFS, attributed to the bottom-up
-        # kernels' share of the run (their summed time per BFS is sec_per_launch * launches)
+        # algorithmic bytes per search: CSR read once + level written once, 4(V+1) + 4 nnz + 4V,
+        # over the time of the whole search (sec_per_launch is the per-step time here)
         V = self.g.V
         nbytes = 4 * (V + 1) + 4 * self.stats["reached_edges"] + 4 * V
-        return {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
-                "traffic": None, "kernel": "bfs_bu_kernel", "algorithmic_bytes_per_bfs": nbytes}
+        achieved = nbytes / sec_per_launch / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "bfs search (bfs_level/hubs/control/b2q kernels)", "algorithmic_bytes_per_bfs": nbytes}
 
     def config(self):
         return {"workload": self.name, "vertices": self.g.V, "nnz": self.g.nnz, "source": 0, "seed": 8201,

@@ -265,20 +265,30 @@ typedef struct {
 
 size_t xd_bfs_workspace_size(int32_t num_vertices, int64_t nnz);
 
+/* Route of a graph for the XCD-aware and rotated BFS modes: the 64-vertex blocks sorted by
+ * the I/O die that homes the start of their adjacency in col (home_attr = xd_home_map() of
+ * col, device; NULL = the address-mask prediction). It depends only on the graph and where
+ * col lives, so it is built once per graph, like the reference's per-vertex work_side map
+ * (applications/bfs/src/bfs.cu:354-409), and reused by every search; rebuild it if col
+ * moves. route: device buffer of xd_bfs_route_bytes(V) bytes, 16-byte aligned. */
+size_t xd_bfs_route_bytes(int32_t num_vertices);
+int xd_bfs_route(const int32_t *rowptr, const int32_t *col, int32_t num_vertices, int64_t nnz,
+                 const uint8_t *home_attr, void *route, size_t route_bytes, void *stream);
+
 /* level[v] = BFS distance from src, XD_BFS_UNVISITED (0xFFFFFFFF) if unreachable, for the
  * undirected graph rowptr[V+1] / col[nnz] (int32, device; every edge stored both ways).
  * Direction-optimizing (top-down queue steps, bottom-up bitmap steps, Beamer's switch with
- * alpha = 14 and beta = 24). Synchronous: the host reads two counters per level. Replaces
- * luo_baseline_level_kernel / luo_side_level_kernel and the host level loops
- * (applications/bfs/src/bfs.cu:215-308, 449-491), which run a fixed number of top-down
- * levels from many sources; the level values follow the same rule (depth + 1 at the first
- * claim, :240, 0xFFFFFFFF unvisited, :30). Modes act on the bottom-up steps:
+ * alpha = 14 and beta = 24, decided on the device; the host reads the control block once per
+ * eight levels). Replaces luo_baseline_level_kernel / luo_side_level_kernel and the host
+ * level loops (applications/bfs/src/bfs.cu:215-308, 449-491), which run a fixed number of
+ * top-down levels from many sources; the level values follow the same rule (depth + 1 at the
+ * first claim, :240, 0xFFFFFFFF unvisited, :30). Modes act on the bottom-up steps:
  * XD_MODE_OBLIVIOUS walks 64-vertex blocks in order; XD_MODE_AWARE gives each I/O die the
- * 64-vertex blocks whose adjacency starts in col memory homed on that die (home_attr =
- * xd_home_map() of col, optional); XD_MODE_ROTATED gives each die the other die's blocks. */
+ * blocks of its route list (route from xd_bfs_route(); NULL = built in this call with the
+ * address-mask prediction); XD_MODE_ROTATED gives each die the other die's blocks. */
 #define XD_BFS_UNVISITED 0xFFFFFFFFu
 int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t num_vertices, int64_t nnz, int32_t src,
-               uint32_t *level, int mode, const uint8_t *home_attr, void *workspace, size_t workspace_bytes,
+               uint32_t *level, int mode, const void *route, void *workspace, size_t workspace_bytes,
                void *stream, xd_bfs_stats_t *stats);
 
 /* ------------------------------------------------------------------------------------ */

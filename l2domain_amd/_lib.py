@@ -86,6 +86,8 @@ SIGNATURES: dict[str, tuple] = {
     "xd_gen_hash_kv": (I, [VP, VP, U64, U64, VP]),
     "xd_gen_hash_queries": (I, [VP, U64, U64, U64, U64, VP]),
     "xd_bfs_workspace_size": (SZ, [C.c_int32, I64]),
+    "xd_bfs_route_bytes": (SZ, [C.c_int32]),
+    "xd_bfs_route": (I, [VP, VP, C.c_int32, I64, VP, VP, SZ, VP]),
     "xd_bfs_csr": (I, [VP, VP, C.c_int32, I64, C.c_int32, VP, I, VP, VP, SZ, VP, C.POINTER(BfsStats)]),
     "xd_rand64": (U64, [U64, U64]),
     "xd_gen_uniform_f32": (I, [VP, SZ, U64]),

@@ -34,7 +34,8 @@ def rmat_csr(scale: int = RMAT_SCALE, edge_factor: int = RMAT_EDGE_FACTOR, seed:
 
 
 class Graph:
-    """CSR graph resident on the device, with its BFS workspace and the home map of col."""
+    """CSR graph resident on the device, with its BFS workspace and its route (the per-die
+    block lists of xd_bfs_route, built once from the measured home map of col)."""
 
     def __init__(self, rowptr: np.ndarray, col: np.ndarray, device: int | str = 0, map_homes: bool = True):
         dev = torch.device(f"cuda:{device}" if isinstance(device, int) else device)
@@ -50,11 +51,14 @@ class Graph:
         if map_homes and self.nnz:
             from .domain import home_map
             self.home_attr = home_map(self.col)
+        self.route = torch.empty(int(_lib.lib.xd_bfs_route_bytes(self.V)), dtype=torch.uint8, device=dev)
+        _lib.call("xd_bfs_route", ptr(self.rowptr), ptr(self.col) if self.nnz else None, self.V, self.nnz,
+                  ptr(self.home_attr), ptr(self.route), self.route.numel(), stream_handle())
 
     def bfs(self, src: int, mode="aware", stream=None) -> tuple[torch.Tensor, dict]:
         st = _lib.BfsStats()
         _lib.call("xd_bfs_csr", ptr(self.rowptr), ptr(self.col) if self.nnz else None, self.V, self.nnz, src,
-                  ptr(self.level), mode_id(mode), ptr(self.home_attr), ptr(self.workspace), self.workspace.numel(),
+                  ptr(self.level), mode_id(mode), ptr(self.route), ptr(self.workspace), self.workspace.numel(),
                   stream_handle(stream), C.byref(st))
         return self.level, {"levels": st.levels, "topdown_steps": st.topdown_steps,
                             "bottomup_steps": st.bottomup_steps, "reached_vertices": st.reached_vertices,

@@ -10,26 +10,30 @@
 //   is searched to completion with Beamer's direction optimisation.
 //
 // MI355X design.
-//   state: level[V]; visited and frontier bitmaps (u64 words, 512 KiB at 2^22 vertices,
-//   resident in every XCD's L2); a frontier queue for top-down steps.
+//   state: level[V]; a visited bitmap and three rotating frontier bitmaps (u64 words, 512 KiB
+//   each at 2^22 vertices, resident in every XCD's L2); two frontier queues; a control block.
+//   Every level writes the next frontier as a bitmap, and a top-down level also as a queue; a
+//   bottom-up level followed by a top-down one is converted to a queue by one extra pass.
+//   Each level zeroes the bitmap the level after it will fill.
 //   top-down: one lane per frontier vertex (hubs above kBigDeg are expanded by the whole
 //     grid in a second kernel); a claim is a 64-bit atomicOr on the visited word; winners
 //     are appended to the next queue with one atomicAdd per wave (ballot + mbcnt).
 //   bottom-up: every unvisited vertex scans its neighbours until one is in the frontier
-//     bitmap; a wave covers 64 vertices and writes their visited/next bits with one atomic
-//     per touched word. Oblivious mode walks 64-vertex blocks in order; XCD-aware mode lets
-//     each I/O die take the blocks whose adjacency starts in memory homed on that die
-//     (xd_home_map of col), so the dominant traffic -- the neighbour lists -- is read from
-//     the near die; rotated hands each die the far blocks.
+//     bitmap; a wave covers one 64-vertex block, i.e. exactly one bitmap word, so it updates
+//     its visited and next words with plain stores. Oblivious mode walks the blocks in order;
+//     XCD-aware mode lets each I/O die take the blocks whose adjacency starts in memory homed
+//     on that die (xd_home_map of col), so the neighbour lists are read from the near die;
+//     rotated hands each die the far blocks.
 //   direction: top-down -> bottom-up when m_f > m_u / 14, bottom-up -> top-down when
-//     n_f < V / 24 (Beamer, Asanovic, Patterson, SC'12), decided on the host after reading
-//     the per-level counters (the call is synchronous).
+//     n_f < V / 24 (Beamer, Asanovic, Patterson, SC'12), decided on the device by a
+//     one-workgroup control kernel after every level. The host enqueues levels in batches
+//     (level, hub expansion, control) and reads the control block once per batch; the
+//     kernels of levels enqueued after the search ended return at once.
 #include <hip/hip_runtime.h>
 
 #include <string.h>
 
 #include <algorithm>
-#include <utility>
 
 #include "xd_common.hpp"
 
@@ -37,58 +41,86 @@ namespace xd {
 
 constexpr uint32_t kUnv = 0xffffffffu;
 constexpr int kBfsThreads = 256;
-constexpr int kBfsGrid = 2048;          // fixed grid of the level kernels (multiple of 8)
-constexpr int32_t kBigDeg = 4096;       // top-down: larger lists are expanded by the whole grid
+constexpr int kBfsGrid = 2048;      // fixed grid of the level kernels (multiple of 8)
+constexpr int kBigGrid = 1024;      // grid of the hub expansion
+constexpr int32_t kBigDeg = 4096;   // top-down: larger lists are expanded by the whole grid
 constexpr double kAlpha = 14.0, kBeta = 24.0;
+constexpr int kLevelBatch = 8;      // levels enqueued per host round trip
+constexpr int kTopDown = 0, kBottomUp = 1, kDone = 2;
 
-struct BfsCounters {
-    unsigned long long next_count;  // vertices appended to the next queue (top-down)
+struct BfsCtl {
+    int32_t dir;    // kTopDown, kBottomUp or kDone
+    int32_t depth;  // completed levels; the running level writes depth + 1
+    int32_t td_steps, bu_steps;
+    long long n_f;  // frontier vertices (the current queue's length)
+    long long m_f;  // frontier edges
+    long long m_u;  // edges of unvisited vertices
+    long long reached_v, reached_e;
+    unsigned long long next_count;  // vertices appended to the next queue in this level
     unsigned long long big_count;   // hub vertices deferred to the grid-wide expansion
+    int32_t convert;                // 1: a bottom-up level is followed by a top-down one
+    int32_t pad;
+    unsigned long long conv_count;  // queue entries written by the bitmap -> queue pass
 };
 
-struct BfsPartial {  // per workgroup, summed by bfs_reduce_kernel
+struct BfsPartial {  // per workgroup, summed by the control kernel
     unsigned long long verts;
     unsigned long long edges;
 };
 
 struct BfsLayout {
-    size_t visited, front_a, front_b, queue_a, queue_b, big, counters, partials, sums, blist, bcount, total;
+    size_t visited, front[3], queue[2], big, ctl, partials, route, total;
     int64_t words, nblocks;
 };
 
 static size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Route buffer: two block counters, then the per-die block lists (nblocks entries each).
+constexpr size_t kRouteHeader = 256;
+static size_t route_bytes(int32_t V) { return kRouteHeader + 2 * 4 * (size_t)(((int64_t)V + 63) / 64); }
+
 static BfsLayout bfs_layout(int32_t V, int64_t nnz) {
     (void)nnz;
     BfsLayout L{};
     L.words = ((int64_t)V + 63) / 64;
+    L.nblocks = ((int64_t)V + 63) / 64;
     size_t o = 0;
-    L.counters = o;
-    o = a256(o + sizeof(BfsCounters));
-    L.sums = o;
-    o = a256(o + sizeof(BfsPartial));
+    L.ctl = o;
+    o = a256(o + sizeof(BfsCtl));
     L.partials = o;
     o = a256(o + sizeof(BfsPartial) * kBfsGrid);
     L.visited = o;
     o = a256(o + 8 * (size_t)L.words);
-    L.front_a = o;
-    o = a256(o + 8 * (size_t)L.words);
-    L.front_b = o;
-    o = a256(o + 8 * (size_t)L.words);
-    L.queue_a = o;
-    o = a256(o + 4 * (size_t)V);
-    L.queue_b = o;
-    o = a256(o + 4 * (size_t)V);
+    for (int i = 0; i < 3; ++i) {
+        L.front[i] = o;
+        o = a256(o + 8 * (size_t)L.words);
+    }
+    for (int i = 0; i < 2; ++i) {
+        L.queue[i] = o;
+        o = a256(o + 4 * (size_t)V);
+    }
     L.big = o;
     o = a256(o + 4 * (size_t)V);
-    L.nblocks = ((int64_t)V + 63) / 64;
-    L.bcount = o;
-    o = a256(o + 2 * sizeof(unsigned long long));
-    L.blist = o;
-    o = a256(o + 2 * 4 * (size_t)L.nblocks);
+    L.route = o;  // per-call block lists when the caller passes no route
+    o = a256(o + route_bytes(V));
     L.total = o;
     return L;
 }
+
+// Device view of the workspace.
+struct BfsState {
+    const int32_t *rowptr;
+    const int32_t *col;
+    int32_t V;
+    int64_t words;
+    uint32_t *level;
+    unsigned long long *visited;
+    unsigned long long *front[3];
+    int32_t *queue[2];
+    int32_t *big;
+    BfsCtl *ctl;
+    BfsPartial *parts;
+};
 
 __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
 #pragma unroll
@@ -96,36 +128,8 @@ __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v)
     return v;
 }
 
-// Sums the per-workgroup partials of a level (one workgroup) into `sums`.
-__global__ void __launch_bounds__(256) bfs_reduce_kernel(const BfsPartial *__restrict__ parts, int n,
-                                                         BfsPartial *__restrict__ sums) {
-    __shared__ unsigned long long sv[256 / kWave], se[256 / kWave];
-    unsigned long long v = 0, e = 0;
-    for (int i = (int)threadIdx.x; i < n; i += 256) {
-        v += parts[i].verts;
-        e += parts[i].edges;
-    }
-    v = wave_sum_u64(v);
-    e = wave_sum_u64(e);
-    const int lane = (int)threadIdx.x % kWave, wave = (int)threadIdx.x / kWave;
-    if (lane == 0) {
-        sv[wave] = v;
-        se[wave] = e;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long tv = 0, te = 0;
-        for (int w = 0; w < 256 / kWave; ++w) {
-            tv += sv[w];
-            te += se[w];
-        }
-        sums->verts = tv;
-        sums->edges = te;
-    }
-}
-
-// Workgroup partial: wave sums through LDS, thread 0 stores (no atomics on one address).
-__device__ __forceinline__ void store_partial(BfsPartial *parts, unsigned long long v, unsigned long long e) {
+// Workgroup sum of (v, e) through LDS; thread 0 gets the totals.
+__device__ __forceinline__ void block_sum2(unsigned long long &v, unsigned long long &e) {
     __shared__ unsigned long long sv[kBfsThreads / kWave], se[kBfsThreads / kWave];
     v = wave_sum_u64(v);
     e = wave_sum_u64(e);
@@ -141,44 +145,48 @@ __device__ __forceinline__ void store_partial(BfsPartial *parts, unsigned long l
             tv += sv[w];
             te += se[w];
         }
-        parts[blockIdx.x].verts = tv;
-        parts[blockIdx.x].edges = te;
+        v = tv;
+        e = te;
     }
 }
 
-__global__ void __launch_bounds__(256) bfs_init_kernel(uint32_t *level, int32_t V, unsigned long long *visited,
-                                                       int64_t words, int32_t src, int32_t *queue) {
+__global__ void __launch_bounds__(256) bfs_init_kernel(BfsState st, int32_t src, int64_t nnz) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < V; i += stride)
-        level[i] = (i == src) ? 0u : kUnv;
-    for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < words; w += stride)
-        visited[w] = (w == src / 64) ? (1ull << (src % 64)) : 0ull;
-    if (blockIdx.x == 0 && threadIdx.x == 0) queue[0] = src;
-}
-
-__global__ void __launch_bounds__(256) bfs_fill_kernel(unsigned long long *p, int64_t n) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0ull;
-}
-
-__global__ void bfs_zero_counters_kernel(BfsCounters *c) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) {
-        c->next_count = 0;
-        c->big_count = 0;
+    const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (int64_t i = t0; i < st.V; i += stride) st.level[i] = (i == src) ? 0u : kUnv;
+    for (int64_t w = t0; w < st.words; w += stride) {
+        const unsigned long long b = (w == src / 64) ? (1ull << (src % 64)) : 0ull;
+        st.visited[w] = b;
+        st.front[0][w] = b;  // level 1 reads front[0] (bottom-up) or queue[0] (top-down)
+        st.front[1][w] = 0ull;
+    }
+    if (t0 == 0) {
+        st.queue[0][0] = src;
+        const long long deg = st.rowptr[src + 1] - st.rowptr[src];
+        BfsCtl c{};
+        c.dir = kTopDown;
+        c.n_f = 1;
+        c.m_f = deg;
+        c.m_u = nnz - deg;
+        c.reached_v = 1;
+        c.reached_e = deg;
+        *st.ctl = c;
     }
 }
 
-// Claims v for level `lvl`; returns true if this thread won it.
+// Claims v for level `lvl`; returns true if this thread won it. Visited bits only go from 0
+// to 1, so a plain (possibly stale) read can only show a set bit as clear; the atomicOr then
+// decides.
 __device__ __forceinline__ bool claim(unsigned long long *visited, uint32_t *level, int32_t v, uint32_t lvl) {
     const unsigned long long bit = 1ull << (v & 63);
     unsigned long long *w = visited + (v >> 6);
-    if (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & bit) return false;
+    if (__hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & bit) return false;
     if (atomicOr(w, bit) & bit) return false;
     level[v] = lvl;
     return true;
 }
 
-// Appends the claiming lanes' vertices to `queue` with one atomic per wave.
+// Appends the lanes' vertices with won == true to `queue` with one atomic per wave.
 __device__ __forceinline__ void wave_append(bool won, int32_t v, int32_t *queue, unsigned long long *count) {
     const uint64_t m = __ballot(won);
     if (!m) return;
@@ -189,136 +197,248 @@ __device__ __forceinline__ void wave_append(bool won, int32_t v, int32_t *queue,
     if (won) queue[base + mask_rank(m)] = v;
 }
 
-__global__ void __launch_bounds__(kBfsThreads)
-bfs_td_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict__ col, const int32_t *__restrict__ queue,
-              int64_t count, uint32_t *__restrict__ level, unsigned long long *__restrict__ visited,
-              int32_t *__restrict__ next, BfsCounters *__restrict__ ctr, int32_t *__restrict__ big,
-              BfsPartial *__restrict__ parts, uint32_t lvl) {
-    unsigned long long my_edges = 0, my_verts = 0;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    // Uniform trip count per wave so that the ballots in wave_append see whole waves.
-    const int64_t first = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~(kWave - 1));
-    for (int64_t i0 = first; i0 < count; i0 += stride) {
-        const int64_t i = i0 + lane_id();
-        int32_t beg = 0, end = 0;
-        if (i < count) {
-            const int32_t u = queue[i];
-            beg = rowptr[u];
-            end = rowptr[u + 1];
-            if (end - beg > kBigDeg) {
-                const unsigned long long slot = atomicAdd(&ctr->big_count, 1ull);
-                big[slot] = u;
-                end = beg;
-            }
-        }
-        // lanes walk their own lists; iterations stay wave-uniform up to the longest list
-        int32_t len = end - beg;
-        int32_t maxlen = len;
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1) maxlen = max(maxlen, __shfl_xor(maxlen, d, kWave));
-        for (int32_t j = 0; j < maxlen; ++j) {
-            bool won = false;
-            int32_t v = 0;
-            if (j < len) {
-                v = col[beg + j];
-                won = claim(visited, level, v, lvl);
-                if (won) {
-                    my_verts += 1;
-                    my_edges += (unsigned long long)(rowptr[v + 1] - rowptr[v]);
-                }
-            }
-            wave_append(won, v, next, &ctr->next_count);
+// A top-down claim of v by this lane: level, visited, next bitmap and next queue.
+__device__ __forceinline__ void td_visit(const BfsState &st, bool have, int32_t v, uint32_t lvl,
+                                         unsigned long long *next_bits, int32_t *next_q,
+                                         unsigned long long &my_verts, unsigned long long &my_edges) {
+    bool won = false;
+    if (have) {
+        won = claim(st.visited, st.level, v, lvl);
+        if (won) {
+            atomicOr(&next_bits[v >> 6], 1ull << (v & 63));
+            my_verts += 1;
+            my_edges += (unsigned long long)(st.rowptr[v + 1] - st.rowptr[v]);
         }
     }
-    store_partial(parts, my_verts, my_edges);
+    wave_append(won, v, next_q, &st.ctl->next_count);
 }
 
-// Grid-wide expansion of the hub vertices deferred by bfs_td_kernel.
-__global__ void __launch_bounds__(kBfsThreads)
-bfs_td_big_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict__ col, const int32_t *__restrict__ big,
-                  const BfsCounters *__restrict__ cnt_in, uint32_t *__restrict__ level,
-                  unsigned long long *__restrict__ visited, int32_t *__restrict__ next, BfsCounters *__restrict__ ctr,
-                  BfsPartial *__restrict__ parts, uint32_t lvl) {
-    unsigned long long my_edges = 0, my_verts = 0;
-    const int64_t nbig = (int64_t)cnt_in->big_count;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t h = 0; h < nbig; ++h) {
-        const int32_t u = big[h];
-        const int32_t beg = rowptr[u], end = rowptr[u + 1];
-        const int64_t first = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~(kWave - 1));
-        for (int64_t e0 = beg + first; e0 < end; e0 += stride) {
-            const int64_t e = e0 + lane_id();
-            bool won = false;
-            int32_t v = 0;
-            if (e < end) {
-                v = col[e];
-                won = claim(visited, level, v, lvl);
-                if (won) {
-                    my_verts += 1;
-                    my_edges += (unsigned long long)(rowptr[v + 1] - rowptr[v]);
-                }
-            }
-            wave_append(won, v, next, &ctr->next_count);
-        }
-    }
-    // add to the partials of the first kernel
-    __shared__ unsigned long long sv[kBfsThreads / kWave], se[kBfsThreads / kWave];
-    my_verts = wave_sum_u64(my_verts);
-    my_edges = wave_sum_u64(my_edges);
-    if (lane_id() == 0) {
-        sv[threadIdx.x / kWave] = my_verts;
-        se[threadIdx.x / kWave] = my_edges;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned long long tv = 0, te = 0;
-        for (int w = 0; w < kBfsThreads / kWave; ++w) {
-            tv += sv[w];
-            te += se[w];
-        }
-        parts[blockIdx.x].verts += tv;
-        parts[blockIdx.x].edges += te;
-    }
-}
-
-// Bottom-up step over the vertices [v0, v1): lanes take v0 + lane, v0 + 64 + lane, ...
-__device__ __forceinline__ void bu_range(int32_t v0, int32_t v1, const int32_t *__restrict__ rowptr,
-                                         const int32_t *__restrict__ col, const unsigned long long *__restrict__ front,
-                                         uint32_t *__restrict__ level, unsigned long long *__restrict__ visited,
-                                         unsigned long long *__restrict__ next, uint32_t lvl,
+// Bottom-up over the 64-vertex block starting at v0 (a multiple of 64): exactly bitmap word
+// v0 / 64, which no other wave touches during this level.
+__device__ __forceinline__ void bu_block(const BfsState &st, int32_t v0, const unsigned long long *front,
+                                         unsigned long long *next_bits, uint32_t lvl,
                                          unsigned long long &my_verts, unsigned long long &my_edges) {
     const int lane = lane_id();
-    for (int32_t vb = v0; vb < v1; vb += kWave) {
-        const int32_t v = vb + lane;
-        bool found = false;
-        int32_t deg = 0;
-        if (v < v1) {
-            const unsigned long long vis = visited[v >> 6];
-            if (!((vis >> (v & 63)) & 1ull)) {
-                const int32_t beg = rowptr[v], end = rowptr[v + 1];
-                deg = end - beg;
-                for (int32_t e = beg; e < end; ++e) {
-                    const int32_t u = col[e];
-                    if ((front[u >> 6] >> (u & 63)) & 1ull) {
-                        found = true;
-                        break;
-                    }
-                }
+    const int32_t v = v0 + lane;
+    const int32_t w0 = v0 >> 6;
+    const unsigned long long vis = st.visited[w0];
+    bool found = false;
+    int32_t deg = 0;
+    if (v < st.V && !((vis >> lane) & 1ull)) {
+        const int32_t beg = st.rowptr[v], end = st.rowptr[v + 1];
+        deg = end - beg;
+        for (int32_t e = beg; e < end; ++e) {
+            const int32_t u = st.col[e];
+            if ((front[u >> 6] >> (u & 63)) & 1ull) {
+                found = true;
+                break;
             }
         }
-        if (found) {
-            level[v] = lvl;
-            my_verts += 1;
-            my_edges += (unsigned long long)deg;
+    }
+    if (found) {
+        st.level[v] = lvl;
+        my_verts += 1;
+        my_edges += (unsigned long long)deg;
+    }
+    const uint64_t m = __ballot(found);
+    if (m && lane == 0) {
+        st.visited[w0] = vis | m;
+        next_bits[w0] = m;
+    }
+}
+
+// One level in the direction the control block names.
+__global__ void __launch_bounds__(kBfsThreads)
+bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const unsigned long long *__restrict__ bcount,
+                 int64_t nblocks) {
+    const int dir = st.ctl->dir;
+    if (dir == kDone) return;
+    const int depth = st.ctl->depth;
+    const uint32_t lvl = (uint32_t)depth + 1;
+    const unsigned long long *cur_bits = st.front[depth % 3];
+    unsigned long long *next_bits = st.front[(depth + 1) % 3];
+    unsigned long long *later_bits = st.front[(depth + 2) % 3];
+    const int32_t *cur_q = st.queue[depth & 1];
+    int32_t *next_q = st.queue[(depth + 1) & 1];
+    const int64_t tstride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t tid0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (int64_t w = tid0; w < st.words; w += tstride) later_bits[w] = 0ull;  // filled by the next level
+
+    unsigned long long my_verts = 0, my_edges = 0;
+    const int wave = (int)threadIdx.x / kWave;
+    constexpr int kWavesPerWg = kBfsThreads / kWave;
+    if (dir == kTopDown) {
+        const int64_t count = st.ctl->n_f;
+        // Uniform trip count per wave so that the ballots in wave_append see whole waves.
+        const int64_t first = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~(kWave - 1));
+        for (int64_t i0 = first; i0 < count; i0 += tstride) {
+            const int64_t i = i0 + lane_id();
+            int32_t beg = 0, end = 0;
+            if (i < count) {
+                const int32_t u = cur_q[i];
+                beg = st.rowptr[u];
+                end = st.rowptr[u + 1];
+                if (end - beg > kBigDeg) {
+                    const unsigned long long slot = atomicAdd(&st.ctl->big_count, 1ull);
+                    st.big[slot] = u;
+                    end = beg;
+                }
+            }
+            // lanes walk their own lists; iterations stay wave-uniform up to the longest list
+            const int32_t len = end - beg;
+            int32_t maxlen = len;
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) maxlen = max(maxlen, __shfl_xor(maxlen, d, kWave));
+            for (int32_t j = 0; j < maxlen; ++j) {
+                const bool have = j < len;
+                const int32_t v = have ? st.col[beg + j] : 0;
+                td_visit(st, have, v, lvl, next_bits, next_q, my_verts, my_edges);
+            }
         }
-        // vb is a multiple of 64, so the block's found bits are exactly bitmap word vb / 64,
-        // which no other wave touches during this step: a plain update suffices
-        const uint64_t m = __ballot(found);
-        if (m && lane == 0) {
-            const int32_t w0 = vb >> 6;
-            visited[w0] |= m;
-            next[w0] |= m;
+    } else if (mode == XD_MODE_OBLIVIOUS) {
+        for (int64_t blk = (int64_t)blockIdx.x * kWavesPerWg + wave; blk < nblocks;
+             blk += (int64_t)gridDim.x * kWavesPerWg)
+            bu_block(st, (int32_t)(blk * kWave), cur_bits, next_bits, lvl, my_verts, my_edges);
+    } else {
+        // The workgroups of a die walk that die's block list (aware) or the other die's
+        // (rotated), so the neighbour lists are read from the near (far) die.
+        const int b = (int)blockIdx.x;
+        const int per_die = (int)gridDim.x / 2;
+        const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
+        const uint32_t die = wg_die(b);
+        const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
+        const int32_t *mine = blist + (int64_t)want * nblocks;
+        const int64_t cnt = (int64_t)bcount[want];
+        for (int64_t i = (int64_t)rank * kWavesPerWg + wave; i < cnt; i += (int64_t)per_die * kWavesPerWg)
+            bu_block(st, mine[i] * kWave, cur_bits, next_bits, lvl, my_verts, my_edges);
+    }
+    block_sum2(my_verts, my_edges);
+    if (threadIdx.x == 0) {
+        st.parts[blockIdx.x].verts = my_verts;
+        st.parts[blockIdx.x].edges = my_edges;
+    }
+}
+
+// Grid-wide expansion of the hub vertices the top-down level deferred.
+__global__ void __launch_bounds__(kBfsThreads) bfs_hubs_kernel(BfsState st) {
+    if (st.ctl->dir != kTopDown) return;
+    const int64_t nbig = (int64_t)st.ctl->big_count;
+    if (nbig == 0) return;
+    const int depth = st.ctl->depth;
+    const uint32_t lvl = (uint32_t)depth + 1;
+    unsigned long long *next_bits = st.front[(depth + 1) % 3];
+    int32_t *next_q = st.queue[(depth + 1) & 1];
+    unsigned long long my_verts = 0, my_edges = 0;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t first = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~(kWave - 1));
+    for (int64_t h = 0; h < nbig; ++h) {
+        const int32_t u = st.big[h];
+        const int32_t beg = st.rowptr[u], end = st.rowptr[u + 1];
+        for (int64_t e0 = beg + first; e0 < end; e0 += stride) {
+            const int64_t e = e0 + lane_id();
+            const bool have = e < end;
+            const int32_t v = have ? st.col[e] : 0;
+            td_visit(st, have, v, lvl, next_bits, next_q, my_verts, my_edges);
         }
+    }
+    block_sum2(my_verts, my_edges);
+    if (threadIdx.x == 0) {  // added to the level kernel's partial of the same index
+        st.parts[blockIdx.x].verts += my_verts;
+        st.parts[blockIdx.x].edges += my_edges;
+    }
+}
+
+// End of a level (one workgroup): sums the partials, advances the depth, picks the next
+// direction and clears the per-level counters.
+__global__ void __launch_bounds__(kBfsThreads) bfs_control_kernel(BfsState st, int nparts) {
+    BfsCtl *c = st.ctl;
+    if (c->dir == kDone) return;
+    unsigned long long v = 0, e = 0;
+    for (int i = (int)threadIdx.x; i < nparts; i += kBfsThreads) {
+        v += st.parts[i].verts;
+        e += st.parts[i].edges;
+    }
+    block_sum2(v, e);
+    if (threadIdx.x != 0) return;
+    const int dir = c->dir;
+    if (dir == kTopDown) ++c->td_steps;
+    else ++c->bu_steps;
+    c->depth += 1;
+    c->n_f = (long long)v;
+    c->m_f = (long long)e;
+    c->next_count = 0;
+    c->big_count = 0;
+    c->convert = 0;
+    c->conv_count = 0;
+    if (v == 0) {
+        c->dir = kDone;
+        return;
+    }
+    c->reached_v += (long long)v;
+    c->reached_e += (long long)e;
+    c->m_u -= (long long)e;
+    if (dir == kTopDown) {
+        if ((double)c->m_f > (double)c->m_u / kAlpha) c->dir = kBottomUp;
+    } else {
+        if ((double)c->n_f < (double)st.V / kBeta) {
+            c->dir = kTopDown;
+            c->convert = 1;  // the new frontier exists only as a bitmap
+        }
+    }
+}
+
+// Bitmap -> queue for a top-down level that follows a bottom-up one: the frontier bitmap of
+// the coming level becomes its queue. A workgroup takes a contiguous range of words and
+// reserves its queue space with one atomic.
+constexpr int kConvWordsPerWg = 1024;
+__global__ void __launch_bounds__(kBfsThreads) bfs_b2q_kernel(BfsState st) {
+    if (st.ctl->convert == 0) return;
+    const int depth = st.ctl->depth;
+    const unsigned long long *bits = st.front[depth % 3];
+    int32_t *q = st.queue[depth & 1];
+    __shared__ uint32_t wtot[kBfsThreads / kWave];
+    __shared__ unsigned long long wbase;
+    const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    for (int64_t w0 = (int64_t)blockIdx.x * kConvWordsPerWg; w0 < st.words;
+         w0 += (int64_t)gridDim.x * kConvWordsPerWg) {
+        // each thread takes 4 consecutive words of the workgroup's 1024
+        unsigned long long m[4];
+        uint32_t c = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t w = w0 + 4 * tid + j;
+            m[j] = w < st.words ? bits[w] : 0ull;
+            c += (uint32_t)__builtin_popcountll(m[j]);
+        }
+        uint32_t incl = c;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const uint32_t t = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += t;
+        }
+        if (lane == kWave - 1) wtot[wave] = incl;
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t tot = 0;
+            for (int k = 0; k < kBfsThreads / kWave; ++k) {
+                const uint32_t x = wtot[k];
+                wtot[k] = tot;
+                tot += x;
+            }
+            wbase = tot ? atomicAdd(&st.ctl->conv_count, (unsigned long long)tot) : 0ull;
+        }
+        __syncthreads();
+        unsigned long long pos = wbase + wtot[wave] + (incl - c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            unsigned long long x = m[j];
+            const int64_t w = w0 + 4 * tid + j;
+            while (x) {
+                q[pos++] = (int32_t)(w * 64 + __builtin_ctzll(x));
+                x &= x - 1;
+            }
+        }
+        __syncthreads();
     }
 }
 
@@ -363,77 +483,23 @@ bfs_blocks_kernel(const int32_t *__restrict__ rowptr, int64_t nblocks, uint64_t 
     }
 }
 
-__global__ void __launch_bounds__(kBfsThreads)
-bfs_bu_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict__ col, int32_t V,
-              const unsigned long long *__restrict__ front, uint32_t *__restrict__ level,
-              unsigned long long *__restrict__ visited, unsigned long long *__restrict__ next, int mode,
-              const int32_t *__restrict__ blist, const unsigned long long *__restrict__ bcount, int64_t nblocks,
-              BfsPartial *__restrict__ parts, uint32_t lvl) {
-    unsigned long long my_verts = 0, my_edges = 0;
-    const int wave = (int)threadIdx.x / kWave;
-    constexpr int kWavesPerWg = kBfsThreads / kWave;
-    if (mode == XD_MODE_OBLIVIOUS) {
-        for (int64_t blk = (int64_t)blockIdx.x * kWavesPerWg + wave; blk < nblocks;
-             blk += (int64_t)gridDim.x * kWavesPerWg) {
-            const int32_t v0 = (int32_t)(blk * kWave);
-            const int32_t v1 = (int32_t)min((int64_t)V, (int64_t)v0 + kWave);
-            bu_range(v0, v1, rowptr, col, front, level, visited, next, lvl, my_verts, my_edges);
-        }
-    } else {
-        // The workgroups of a die walk that die's block list (aware) or the other die's
-        // (rotated), so the neighbour lists are read from the near (far) die.
-        const int b = (int)blockIdx.x;
-        const int per_die = (int)gridDim.x / 2;
-        const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
-        const uint32_t die = wg_die(b);
-        const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
-        const int32_t *mine = blist + (int64_t)want * nblocks;
-        const int64_t cnt = (int64_t)bcount[want];
-        for (int64_t i = (int64_t)rank * kWavesPerWg + wave; i < cnt; i += (int64_t)per_die * kWavesPerWg) {
-            const int32_t v0 = mine[i] * kWave;
-            const int32_t v1 = (int32_t)min((int64_t)V, (int64_t)v0 + kWave);
-            bu_range(v0, v1, rowptr, col, front, level, visited, next, lvl, my_verts, my_edges);
-        }
-    }
-    store_partial(parts, my_verts, my_edges);
+__global__ void bfs_clear2_kernel(unsigned long long *p) {
+    if (threadIdx.x < 2) p[threadIdx.x] = 0ull;
 }
 
-// queue -> bitmap (top-down to bottom-up switch)
-__global__ void __launch_bounds__(256) bfs_q2b_kernel(const int32_t *__restrict__ queue, int64_t count,
-                                                      unsigned long long *__restrict__ bits) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
-        const int32_t v = queue[i];
-        atomicOr(&bits[v >> 6], 1ull << (v & 63));
-    }
-}
-
-// bitmap -> queue (bottom-up to top-down switch); one atomic per wave
-__global__ void __launch_bounds__(256) bfs_b2q_kernel(const unsigned long long *__restrict__ bits, int64_t words,
-                                                      int32_t *__restrict__ queue, unsigned long long *__restrict__ count) {
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const int64_t first = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~(kWave - 1));
-    for (int64_t w0 = first; w0 < words; w0 += stride) {
-        const int64_t w = w0 + lane_id();
-        unsigned long long m = w < words ? bits[w] : 0ull;
-        const uint32_t c = (uint32_t)__builtin_popcountll(m);
-        // exclusive wave scan of c
-        uint32_t incl = c;
-#pragma unroll
-        for (int d = 1; d < kWave; d <<= 1) {
-            const uint32_t t = __shfl_up(incl, d, kWave);
-            if (lane_id() >= d) incl += t;
-        }
-        const uint32_t total = (uint32_t)__shfl(incl, kWave - 1, kWave);
-        unsigned long long base = 0;
-        if (lane_id() == 0 && total) base = atomicAdd(count, (unsigned long long)total);
-        base = __shfl(base, 0, kWave) + (incl - c);
-        while (m) {
-            const int bit = __builtin_ctzll(m);
-            queue[base++] = (int32_t)(w * 64 + bit);
-            m &= m - 1;
-        }
-    }
+// Per-die block lists of a graph into `route` (header: the two counts).
+static int build_route(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz, const uint8_t *home_attr,
+                       void *route, hipStream_t s) {
+    const int64_t nblocks = ((int64_t)V + 63) / 64;
+    auto *bcount = static_cast<unsigned long long *>(route);
+    auto *blist = reinterpret_cast<int32_t *>(static_cast<char *>(route) + kRouteHeader);
+    hipLaunchKernelGGL(bfs_clear2_kernel, dim3(1), dim3(64), 0, s, bcount);
+    if (nnz == 0) return launch_status("bfs_clear2_kernel");
+    const HomeMap home{home_attr, reinterpret_cast<uint64_t>(col) / kHomePage, home_mask()};
+    hipLaunchKernelGGL(bfs_blocks_kernel, dim3((unsigned)((nblocks + kBlkThreads - 1) / kBlkThreads)), dim3(kBlkThreads),
+                       0, s, rowptr, nblocks, reinterpret_cast<uint64_t>(col), nnz * (int64_t)sizeof(int32_t), home, blist,
+                       bcount);
+    return launch_status("bfs_blocks_kernel");
 }
 
 }  // namespace xd
@@ -447,8 +513,18 @@ size_t xd_bfs_workspace_size(int32_t num_vertices, int64_t nnz) {
     return bfs_layout(num_vertices, nnz).total;
 }
 
+size_t xd_bfs_route_bytes(int32_t num_vertices) { return num_vertices > 0 ? route_bytes(num_vertices) : 0; }
+
+int xd_bfs_route(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz, const uint8_t *home_attr,
+                 void *route, size_t route_bytes_avail, void *stream) {
+    XD_REQUIRE(rowptr != nullptr && route != nullptr && (nnz == 0 || col != nullptr), "xd_bfs_route: NULL pointer");
+    XD_REQUIRE(V > 0 && nnz >= 0 && nnz < (1ll << 31), "xd_bfs_route: need 0 < V and 0 <= nnz < 2^31");
+    XD_REQUIRE(route_bytes_avail >= route_bytes(V) && aligned16(route), "xd_bfs_route: route buffer too small");
+    return build_route(rowptr, col, V, nnz, home_attr, route, (hipStream_t)stream);
+}
+
 int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz, int32_t src, uint32_t *level,
-               int mode, const uint8_t *home_attr, void *workspace, size_t workspace_bytes, void *stream,
+               int mode, const void *route, void *workspace, size_t workspace_bytes, void *stream,
                xd_bfs_stats_t *stats) {
     XD_REQUIRE(rowptr != nullptr && level != nullptr && (nnz == 0 || col != nullptr), "xd_bfs_csr: NULL pointer");
     XD_REQUIRE(V > 0 && nnz >= 0 && nnz < (1ll << 31), "xd_bfs_csr: need 0 < V and 0 <= nnz < 2^31");
@@ -459,105 +535,58 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
         return fail(XD_ERR_WORKSPACE, "xd_bfs_csr: workspace missing or smaller than xd_bfs_workspace_size()");
     hipStream_t s = (hipStream_t)stream;
     char *ws = static_cast<char *>(workspace);
-    auto *visited = reinterpret_cast<unsigned long long *>(ws + L.visited);
-    auto *fa = reinterpret_cast<unsigned long long *>(ws + L.front_a);
-    auto *fb = reinterpret_cast<unsigned long long *>(ws + L.front_b);
-    auto *qa = reinterpret_cast<int32_t *>(ws + L.queue_a);
-    auto *qb = reinterpret_cast<int32_t *>(ws + L.queue_b);
-    auto *big = reinterpret_cast<int32_t *>(ws + L.big);
-    auto *ctr = reinterpret_cast<BfsCounters *>(ws + L.counters);
-    auto *parts = reinterpret_cast<BfsPartial *>(ws + L.partials);
-    auto *sums = reinterpret_cast<BfsPartial *>(ws + L.sums);
-    auto *blist = reinterpret_cast<int32_t *>(ws + L.blist);
-    auto *bcount = reinterpret_cast<unsigned long long *>(ws + L.bcount);
-    const HomeMap home{nnz > 0 ? home_attr : nullptr, reinterpret_cast<uint64_t>(col) / kHomePage, home_mask()};
+    BfsState st{};
+    st.rowptr = rowptr;
+    st.col = col;
+    st.V = V;
+    st.words = L.words;
+    st.level = level;
+    st.visited = reinterpret_cast<unsigned long long *>(ws + L.visited);
+    for (int i = 0; i < 3; ++i) st.front[i] = reinterpret_cast<unsigned long long *>(ws + L.front[i]);
+    for (int i = 0; i < 2; ++i) st.queue[i] = reinterpret_cast<int32_t *>(ws + L.queue[i]);
+    st.big = reinterpret_cast<int32_t *>(ws + L.big);
+    st.ctl = reinterpret_cast<BfsCtl *>(ws + L.ctl);
+    st.parts = reinterpret_cast<BfsPartial *>(ws + L.partials);
     const int bmode = nnz > 0 ? mode : XD_MODE_OBLIVIOUS;  // no adjacency to route by
     const unsigned g256 = (unsigned)std::min<int64_t>(8192, ((int64_t)V + 255) / 256 + 1);
-
-    int32_t src_rows[2];
-    XD_HIP(hipMemcpyAsync(src_rows, rowptr + src, sizeof(src_rows), hipMemcpyDeviceToHost, s));
-    XD_HIP(hipStreamSynchronize(s));
+    const void *rt = route;
     {
         KernelTimer kt("bfs_init", s);
-        hipLaunchKernelGGL(bfs_init_kernel, dim3(g256), dim3(256), 0, s, level, V, visited, L.words, src, qa);
+        hipLaunchKernelGGL(bfs_init_kernel, dim3(g256), dim3(256), 0, s, st, src, nnz);
         if (int rc = launch_status("bfs_init_kernel")) return rc;
-        if (bmode != XD_MODE_OBLIVIOUS) {
-            hipLaunchKernelGGL(bfs_fill_kernel, dim3(1), dim3(64), 0, s, bcount, (int64_t)2);
-            hipLaunchKernelGGL(bfs_blocks_kernel, dim3((unsigned)((L.nblocks + kBlkThreads - 1) / kBlkThreads)),
-                               dim3(kBlkThreads), 0, s, rowptr, L.nblocks, reinterpret_cast<uint64_t>(col),
-                               nnz * (int64_t)sizeof(int32_t), home, blist, bcount);
-            if (int rc = launch_status("bfs_blocks_kernel")) return rc;
+        if (bmode != XD_MODE_OBLIVIOUS && rt == nullptr) {  // no prepared route: build one here
+            if (int rc = build_route(rowptr, col, V, nnz, nullptr, ws + L.route, s)) return rc;
+            rt = ws + L.route;
         }
     }
-    int64_t m_u = nnz - (src_rows[1] - src_rows[0]);
-    int64_t n_f = 1, m_f = src_rows[1] - src_rows[0];
-    int64_t reached_v = 1, reached_e = m_f;
-    bool bottom_up = false;
-    int32_t *qcur = qa, *qnext = qb;
-    unsigned long long *fcur = fa, *fnext = fb;
-    int td = 0, bu = 0, depth = 0;
-    for (;; ++depth) {
-        const uint32_t lvl = (uint32_t)depth + 1;
-        hipLaunchKernelGGL(bfs_zero_counters_kernel, dim3(1), dim3(64), 0, s, ctr);
-        if (!bottom_up) {
-            ++td;
+    const auto *bcount = static_cast<const unsigned long long *>(rt);
+    const auto *blist =
+        rt ? reinterpret_cast<const int32_t *>(static_cast<const char *>(rt) + kRouteHeader) : nullptr;
+    const unsigned conv_grid = (unsigned)std::min<int64_t>(512, (L.words + kConvWordsPerWg - 1) / kConvWordsPerWg);
+    BfsCtl h{};
+    for (int64_t enq = 0;;) {
+        for (int k = 0; k < kLevelBatch; ++k, ++enq) {
             {
-                KernelTimer kt("bfs_topdown", s);
-                hipLaunchKernelGGL(bfs_td_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, rowptr, col, qcur, n_f,
-                                   level, visited, qnext, ctr, big, parts, lvl);
-                if (int rc = launch_status("bfs_td_kernel")) return rc;
-                hipLaunchKernelGGL(bfs_td_big_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, rowptr, col, big, ctr,
-                                   level, visited, qnext, ctr, parts, lvl);
-                if (int rc = launch_status("bfs_td_big_kernel")) return rc;
+                KernelTimer kt("bfs_level", s);
+                hipLaunchKernelGGL(bfs_level_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, st, bmode, blist, bcount,
+                                   L.nblocks);
             }
-        } else {
-            ++bu;
-            KernelTimer kt("bfs_bottomup", s);
-            hipLaunchKernelGGL(bfs_fill_kernel, dim3((unsigned)std::min<int64_t>(2048, L.words / 256 + 1)), dim3(256), 0,
-                               s, fnext, L.words);
-            hipLaunchKernelGGL(bfs_bu_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, rowptr, col, V, fcur, level,
-                               visited, fnext, bmode, blist, bcount, L.nblocks, parts, lvl);
-            if (int rc = launch_status("bfs_bu_kernel")) return rc;
+            hipLaunchKernelGGL(bfs_hubs_kernel, dim3(kBigGrid), dim3(kBfsThreads), 0, s, st);
+            hipLaunchKernelGGL(bfs_control_kernel, dim3(1), dim3(kBfsThreads), 0, s, st, kBfsGrid);
+            hipLaunchKernelGGL(bfs_b2q_kernel, dim3(conv_grid), dim3(kBfsThreads), 0, s, st);
+            if (int rc = launch_status("bfs level kernels")) return rc;
         }
-        hipLaunchKernelGGL(bfs_reduce_kernel, dim3(1), dim3(256), 0, s, parts, kBfsGrid, sums);
-        BfsPartial h{};
-        XD_HIP(hipMemcpyAsync(&h, sums, sizeof(h), hipMemcpyDeviceToHost, s));
+        XD_HIP(hipMemcpyAsync(&h, st.ctl, sizeof(h), hipMemcpyDeviceToHost, s));
         XD_HIP(hipStreamSynchronize(s));
-        n_f = (int64_t)h.verts;
-        m_f = (int64_t)h.edges;
-        if (n_f == 0) break;
-        reached_v += n_f;
-        reached_e += m_f;
-        m_u -= m_f;
-        if (!bottom_up) {
-            if ((double)m_f > (double)m_u / kAlpha) {
-                bottom_up = true;
-                hipLaunchKernelGGL(bfs_fill_kernel, dim3((unsigned)std::min<int64_t>(2048, L.words / 256 + 1)), dim3(256),
-                                   0, s, fcur, L.words);
-                hipLaunchKernelGGL(bfs_q2b_kernel, dim3((unsigned)std::min<int64_t>(4096, n_f / 256 + 1)), dim3(256), 0, s,
-                                   qnext, n_f, fcur);
-                if (int rc = launch_status("bfs_q2b_kernel")) return rc;
-            } else {
-                std::swap(qcur, qnext);
-            }
-        } else {
-            if ((double)n_f < (double)V / kBeta) {
-                bottom_up = false;
-                hipLaunchKernelGGL(bfs_zero_counters_kernel, dim3(1), dim3(64), 0, s, ctr);
-                hipLaunchKernelGGL(bfs_b2q_kernel, dim3((unsigned)std::min<int64_t>(4096, L.words / 256 + 1)), dim3(256), 0,
-                                   s, fnext, L.words, qcur, &ctr->next_count);
-                if (int rc = launch_status("bfs_b2q_kernel")) return rc;
-            } else {
-                std::swap(fcur, fnext);
-            }
-        }
+        if (h.dir == kDone) break;
+        if (enq > (int64_t)V + 1) return fail(XD_ERR_INCOMPLETE, "xd_bfs_csr: search did not finish");
     }
     if (stats) {
-        stats->levels = depth + 1;
-        stats->topdown_steps = td;
-        stats->bottomup_steps = bu;
-        stats->reached_vertices = reached_v;
-        stats->reached_edges = reached_e;
+        stats->levels = h.depth;
+        stats->topdown_steps = h.td_steps;
+        stats->bottomup_steps = h.bu_steps;
+        stats->reached_vertices = h.reached_v;
+        stats->reached_edges = h.reached_e;
     }
     return XD_OK;
 }

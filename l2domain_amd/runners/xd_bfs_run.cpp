@@ -68,6 +68,9 @@ int main(int argc, char **argv) {
     void *ws;
     RUN_HIP(hipMalloc(&ws, wsb));
     HomeMap home(dcol, (size_t)std::max<int64_t>(nnz, 1) * 4, s);
+    void *route;  // per-die block lists, built once per graph
+    RUN_HIP(hipMalloc(&route, xd_bfs_route_bytes(V)));
+    RUN_XD(xd_bfs_route(drow, dcol, V, nnz, home.attr, route, xd_bfs_route_bytes(V), s));
 
     // serial queue BFS of the first source
     const auto t0 = std::chrono::steady_clock::now();
@@ -92,7 +95,7 @@ int main(int argc, char **argv) {
     long long bad[3] = {0, 0, 0};
     std::vector<uint32_t> got[3];
     for (int mode = 0; mode < 3; ++mode) {
-        RUN_XD(xd_bfs_csr(drow, dcol, V, nnz, 0, lvl[mode], mode, home.attr, ws, wsb, s, &st));
+        RUN_XD(xd_bfs_csr(drow, dcol, V, nnz, 0, lvl[mode], mode, route, ws, wsb, s, &st));
         got[mode].resize(V);
         RUN_HIP(hipMemcpy(got[mode].data(), lvl[mode], (size_t)V * 4, hipMemcpyDeviceToHost));
     }
@@ -110,7 +113,7 @@ int main(int argc, char **argv) {
             double edges = 0;
             const float t = time_ms(s, [&] {
                 for (int k = 0; k < nsrc; ++k) {
-                    RUN_XD(xd_bfs_csr(drow, dcol, V, nnz, k, lvl[mode], mode, home.attr, ws, wsb, s, &st));
+                    RUN_XD(xd_bfs_csr(drow, dcol, V, nnz, k, lvl[mode], mode, route, ws, wsb, s, &st));
                     edges += st.reached_edges / 2.0;
                 }
             });

@@ -91,3 +91,21 @@ def test_config_rmat22(config_graph, mode):
     np.testing.assert_array_equal(level.cpu().numpy().view(np.uint32), ref)
     assert st["reached_vertices"] == reached
     assert st["bottomup_steps"] >= 1 and st["topdown_steps"] >= 1
+
+
+def test_route_and_per_call_lists_agree():
+    # aware/rotated with the prepared route (measured homes) and with per-call lists
+    # (address-mask homes, route=None) give the same levels as the serial oracle
+    import ctypes as C
+    from l2domain_amd import _lib
+    from l2domain_amd._torch import mode_id, ptr, stream_handle
+    rowptr, col = rmat_csr(14, 8, 99)
+    ref, _ = ora.bfs(rowptr, col, 5)
+    g = Graph(rowptr, col)
+    for mode in ("aware", "rotated"):
+        lev, _ = g.bfs(5, mode=mode)
+        np.testing.assert_array_equal(lev.cpu().numpy().view(np.uint32), ref)
+        st = _lib.BfsStats()
+        _lib.call("xd_bfs_csr", ptr(g.rowptr), ptr(g.col), g.V, g.nnz, 5, ptr(g.level), mode_id(mode), None,
+                  ptr(g.workspace), g.workspace.numel(), stream_handle(), C.byref(st))
+        np.testing.assert_array_equal(g.level.cpu().numpy().view(np.uint32), ref)

@@ -308,6 +308,70 @@ class Hash:
                 "sample": "2^23 serial inserts into 2^24 slots + 2^23 lookups (oracle, HASH.cu:46-64,226-241)"}
 
 
+class HashDep:
+    """The reference's own hash workload (hash_probe_dep.cu, defaults :124-130): K = 32000000
+    int32 keys with successors in 2^26 8-byte entries, two hot pools of 100000 keys homed on
+    opposite I/O dies, 8000000 queries (80 % hot) following their chains for 4 dependent
+    probes. A step = one probe pass."""
+    name = "hash_dep_K32M_Q8M_C2p26_L4"
+    unit = "Mprobes/s"
+    dtype = "int32"
+    dominant = "dep_probe"
+    single_kernel = True
+
+    def __init__(self, K=32000000, Q=8000000, slots=1 << 26, L=4, hot=80, H=100000):
+        import torch
+        from l2domain_amd.hashdep import DepTable
+        self.K, self.Q, self.slots, self.L, self.hot, self.H = K, Q, slots, L, hot, H
+        t0 = time.perf_counter()
+        self.t = DepTable(K, slots, H)
+        self.hq = self.t.queries(Q, hot)
+        self.build_s = time.perf_counter() - t0
+        self.q = torch.from_numpy(self.hq).cuda()
+        self.out = torch.empty(Q, dtype=torch.int32, device="cuda")
+
+    def step(self, mode):
+        self.t.probe(self.q, self.L, mode=mode, out=self.out)
+
+    def throughput(self, sec_per_step):
+        return self.Q * self.L / sec_per_step / 1e6
+
+    def verify(self):
+        import numpy as np
+        import oracle as ora
+        ref = ora.dep_probe(self.t.host_table, self.slots, self.hq, self.L)
+        ok = True
+        for mode in MODES:
+            self.step(mode)
+            ok = ok and bool(np.array_equal(self.out.cpu().numpy(), ref))
+        return ok
+
+    def roofline(self, sec_per_launch):
+        # latency-bound dependent chains: algorithmic bytes = 8 B entry per probe + 4 B query
+        # in + 4 B out per query
+        nbytes = 8 * self.Q * self.L + 8 * self.Q
+        achieved = nbytes / sec_per_launch / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "dep_probe_kernel",
+                "algorithmic_bytes_per_launch": nbytes}
+
+    def config(self):
+        return {"workload": self.name, "K": self.K, "Q": self.Q, "C": self.slots, "L": self.L, "hot_pct": self.hot,
+                "H": self.H, "seed": 42, "host_build_s": round(self.build_s, 2)}
+
+    def cpu_baseline(self):
+        import oracle as ora
+        n = 1 << 20
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 5.0:
+            ora.dep_probe(self.t.host_table, self.slots, self.hq[:n], self.L)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(n * self.L / dt / 1e6, 3), "unit": "Mprobes/s", "cores": 1, "kind": "port",
+                "sample": f"{reps} x 2^20 queries of the same stream (oracle probe_dep_base loop, HASH.cu:66-83)"}
+
+
 class Bfs:
     """undirected R-MAT scale 22, edge factor 16, a/b/c/d = .57/.19/.19/.05 (seed
     8201), CSR int32, source 0. A step = one BFS to completion."""
@@ -373,6 +437,7 @@ WORKLOADS = {
     "hist": Hist,
     "bfs": Bfs,
     "hash": Hash,
+    "hash_dep": HashDep,
     "gemv_f32": GemvF32,
     "gemv_f16_up": lambda: GemvF16(14336, 4096),
     "gemv_f16_down": lambda: GemvF16(4096, 14336),
@@ -380,7 +445,8 @@ WORKLOADS = {
 DEFAULT_WORKLOAD = "hist"
 # every other BASELINE config, reported under "extras" of the same JSON line
 EXTRAS = (("gemv_f32", False), ("gemv_f32", True), ("gemv_f16_up", False), ("gemv_f16_up", True),
-          ("gemv_f16_down", False), ("gemv_f16_down", True), ("hash", False), ("bfs", False))
+          ("gemv_f16_down", False), ("gemv_f16_down", True), ("hash", False), ("hash_dep", False),
+          ("bfs", False))
 
 
 # ---------------------------------------------------------------------------------------

@@ -252,6 +252,31 @@ int xd_gen_hash_kv(uint64_t *keys, uint64_t *vals, uint64_t n, uint64_t seed, vo
 int xd_gen_hash_queries(uint64_t *queries, uint64_t n, uint64_t n_keys, uint64_t seed, uint64_t qseed,
                         void *stream);
 
+/* The reference's own hash workload (applications/hash/src/hash_probe_dep.cu), as an input
+ * mode: a table of `slots` 8-byte entries {int32 key; int32 next} (EMPTY key = -1), home slot
+ * mix32(key) & (slots - 1) (lowbias32), linear probing.
+ * xd_dep_make_keys (host): K keys with successors -- two hot pools of H odd keys whose home
+ *   slots lie on I/O die 0 and die 1 of the table at device address table_addr (home_attr_host
+ *   = a host copy of xd_home_map() of the table, NULL = address-mask prediction), each chained
+ *   into a cycle, then cold keys that are their own successor (HASH.cu:194-224).
+ * xd_dep_build (host): table[2 * slots] filled by serial insertion in the order of a
+ *   Fisher-Yates shuffle driven by xd_rand64(seed, i) (HASH.cu:226-241).
+ * xd_dep_queries (host): the first hot_pct percent of the Q queries alternate the hot pools
+ *   (even: die-0 pool), the rest are uniform over all keys (HASH.cu:244-270).
+ * xd_dep_probe (device): out[i] = (sum over chain_len dependent probes of the found slot, or
+ *   -1 for a missing key, wrapping) ^ the final key (probe_chain_one / probe_dep_base,
+ *   HASH.cu:46-83). XD_MODE_AWARE routes every query to the die that homes its first slot
+ *   (probe_dep_sa with per-side query lists, :85-116, with the routing done on the device);
+ *   XD_MODE_ROTATED to the other die. home_attr: xd_home_map() of the table (device). */
+int xd_dep_make_keys(uint64_t table_addr, uint64_t slots, const uint8_t *home_attr_host, int32_t K, int32_t H,
+                     int32_t *keys, int32_t *nexts);
+int xd_dep_build(int32_t *table, uint64_t slots, const int32_t *keys, const int32_t *nexts, int32_t K,
+                 uint64_t seed);
+int xd_dep_queries(int32_t *queries, int32_t Q, const int32_t *keys, int32_t K, int32_t H, int32_t hot_pct,
+                   uint64_t seed);
+int xd_dep_probe(const void *table, uint64_t slots, const int32_t *queries, uint64_t n, int chain_len,
+                 int32_t *out, int mode, const uint8_t *home_attr, void *stream);
+
 /* ------------------------------------------------------------------------------------ */
 /* BFS over an undirected CSR graph                                                       */
 /* ------------------------------------------------------------------------------------ */
@@ -278,8 +303,8 @@ int xd_bfs_route(const int32_t *rowptr, const int32_t *col, int32_t num_vertices
 /* level[v] = BFS distance from src, XD_BFS_UNVISITED (0xFFFFFFFF) if unreachable, for the
  * undirected graph rowptr[V+1] / col[nnz] (int32, device; every edge stored both ways).
  * Direction-optimizing (top-down queue steps, bottom-up bitmap steps, Beamer's switch with
- * alpha = 14 and beta = 24, decided on the device; the host reads the control block once per
- * eight levels). Replaces luo_baseline_level_kernel / luo_side_level_kernel and the host
+ * alpha = 14 and beta = 24, decided on the device; the host reads the control block after six
+ * levels and then after every four). Replaces luo_baseline_level_kernel / luo_side_level_kernel and the host
  * level loops (applications/bfs/src/bfs.cu:215-308, 449-491), which run a fixed number of
  * top-down levels from many sources; the level values follow the same rule (depth + 1 at the
  * first claim, :240, 0xFFFFFFFF unvisited, :30). Modes act on the bottom-up steps:

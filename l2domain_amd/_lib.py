@@ -85,6 +85,10 @@ SIGNATURES: dict[str, tuple] = {
     "xd_hash_lookup_u64": (I, [VP, U64, VP, U64, VP, VP, I, VP, VP]),
     "xd_gen_hash_kv": (I, [VP, VP, U64, U64, VP]),
     "xd_gen_hash_queries": (I, [VP, U64, U64, U64, U64, VP]),
+    "xd_dep_make_keys": (I, [U64, U64, VP, C.c_int32, C.c_int32, VP, VP]),
+    "xd_dep_build": (I, [VP, U64, VP, VP, C.c_int32, U64]),
+    "xd_dep_queries": (I, [VP, C.c_int32, VP, C.c_int32, C.c_int32, C.c_int32, U64]),
+    "xd_dep_probe": (I, [VP, U64, VP, U64, I, VP, I, VP, VP]),
     "xd_bfs_workspace_size": (SZ, [C.c_int32, I64]),
     "xd_bfs_route_bytes": (SZ, [C.c_int32]),
     "xd_bfs_route": (I, [VP, VP, C.c_int32, I64, VP, VP, SZ, VP]),

@@ -27,7 +27,8 @@
 //   direction: top-down -> bottom-up when m_f > m_u / 14, bottom-up -> top-down when
 //     n_f < V / 24 (Beamer, Asanovic, Patterson, SC'12), decided on the device by a
 //     one-workgroup control kernel after every level. The host enqueues levels in batches
-//     (level, hub expansion, control) and reads the control block once per batch; the
+//     (level, hub expansion, control, conversion) of six, then four, and reads the control
+//     block once per batch; the
 //     kernels of levels enqueued after the search ended return at once.
 #include <hip/hip_runtime.h>
 
@@ -45,7 +46,8 @@ constexpr int kBfsGrid = 2048;      // fixed grid of the level kernels (multiple
 constexpr int kBigGrid = 1024;      // grid of the hub expansion
 constexpr int32_t kBigDeg = 4096;   // top-down: larger lists are expanded by the whole grid
 constexpr double kAlpha = 14.0, kBeta = 24.0;
-constexpr int kLevelBatch = 8;      // levels enqueued per host round trip
+constexpr int kFirstBatch = 6;      // levels enqueued before the first host round trip
+constexpr int kLevelBatch = 4;      // levels enqueued per later round trip
 constexpr int kTopDown = 0, kBottomUp = 1, kDone = 2;
 
 struct BfsCtl {
@@ -565,7 +567,8 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     const unsigned conv_grid = (unsigned)std::min<int64_t>(512, (L.words + kConvWordsPerWg - 1) / kConvWordsPerWg);
     BfsCtl h{};
     for (int64_t enq = 0;;) {
-        for (int k = 0; k < kLevelBatch; ++k, ++enq) {
+        const int batch = enq == 0 ? kFirstBatch : kLevelBatch;
+        for (int k = 0; k < batch; ++k, ++enq) {
             {
                 KernelTimer kt("bfs_level", s);
                 hipLaunchKernelGGL(bfs_level_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, st, bmode, blist, bcount,

@@ -205,6 +205,68 @@ hash_lookup_kernel(const Slot *__restrict__ table, uint64_t mask, const uint64_t
     for_each_owned(w, n, filter, queues[threadIdx.x / kWave], key_of, keep, body);
 }
 
+// ---------------------------------------------------------------------------------------
+// The reference's dependent-probe workload (hash_probe_dep.cu): 8-byte entries {int key;
+// int next}, EMPTY key -1, home slot mix32(key) & mask, linear probing; a query follows its
+// key's `next` chain for chain_len probes and returns (sum of found slots, -1 for a miss) ^
+// final key. The aware mode routes each query to the die that homes its first slot.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t mix32d(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+// probe_chain_one (HASH.cu:46-64): the found slot or -1, and the key's successor (the key
+// itself when it is absent).
+__device__ __forceinline__ int32_t dep_probe_one(const int2 *__restrict__ table, uint32_t mask, int32_t key,
+                                                 int32_t &next) {
+    uint32_t slot = mix32d((uint32_t)key) & mask;
+    bool found = false;
+    int32_t nk = key;
+    for (uint64_t step = 0; step <= (uint64_t)mask; ++step) {
+        const int2 e = table[slot];
+        if (e.x == key) {
+            found = true;
+            nk = e.y;
+            break;
+        }
+        if (e.x == -1) break;
+        slot = (slot + 1) & mask;
+    }
+    next = nk;
+    return found ? (int32_t)slot : -1;
+}
+
+__global__ void __launch_bounds__(kHashThreads)
+dep_probe_kernel(const int2 *__restrict__ table, uint32_t mask, const int32_t *__restrict__ queries, uint64_t n,
+                 int chain_len, int32_t *__restrict__ out, int mode, HomeMap home) {
+    __shared__ uint32_t queues[kHashThreads / kWave][2 * kWave];
+    __shared__ uint8_t lattr[kLdsPages];
+    const Walk w = make_walk(mode);
+    const bool filter = mode != XD_MODE_OBLIVIOUS;
+    const uint64_t base = reinterpret_cast<uint64_t>(table);
+    const SlotHome sh = stage_home(home, base, ((uint64_t)mask + 1) * sizeof(int2), lattr, filter);
+    auto key_of = [&](uint64_t i) { return (uint64_t)(uint32_t)queries[i]; };
+    auto keep = [&](uint64_t key) {
+        return sh(base + (uint64_t)(mix32d((uint32_t)key) & mask) * sizeof(int2)) == w.want;
+    };
+    auto body = [&](uint64_t i) {
+        int32_t key = queries[i];
+        uint32_t acc = 0;  // wraps like the reference's int accumulator
+        for (int it = 0; it < chain_len; ++it) {
+            int32_t nk;
+            acc += (uint32_t)dep_probe_one(table, mask, key, nk);
+            key = nk;
+        }
+        out[i] = (int32_t)(acc ^ (uint32_t)key);
+    };
+    for_each_owned(w, n, filter, queues[threadIdx.x / kWave], key_of, keep, body);
+}
+
 // Seeded inputs (device): key i = splitmix64(seed, i) (distinct for distinct i),
 // value i = splitmix64(seed ^ 0x5BD1E9955BD1E995, i); query j is a hit for even j
 // (key splitmix64(qseed, j) mod n_keys) and a miss for odd j (key n_keys + j/2, from the
@@ -295,6 +357,22 @@ int xd_hash_lookup_u64(const void *table, uint64_t slots, const uint64_t *querie
                        HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()}, vals_out,
                        found_out);
     return launch_status("hash_lookup_kernel");
+}
+
+int xd_dep_probe(const void *table, uint64_t slots, const int32_t *queries, uint64_t n, int chain_len, int32_t *out,
+                 int mode, const uint8_t *home_attr, void *stream) {
+    XD_REQUIRE(table != nullptr && (reinterpret_cast<uintptr_t>(table) & 7u) == 0, "xd_dep_probe: table must be 8-byte aligned");
+    XD_REQUIRE(slots >= 2 && (slots & (slots - 1)) == 0 && slots <= (1ull << 32), "xd_dep_probe: slots must be a power of two <= 2^32");
+    XD_REQUIRE(n == 0 || (queries != nullptr && out != nullptr), "xd_dep_probe: NULL queries/out");
+    XD_REQUIRE(n < (1ull << 32), "xd_dep_probe: n must be < 2^32");
+    XD_REQUIRE(chain_len >= 1 && chain_len <= 4096, "xd_dep_probe: chain_len must be in [1, 4096]");
+    XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_dep_probe: bad mode");
+    if (n == 0) return XD_OK;
+    KernelTimer kt("dep_probe", (hipStream_t)stream);
+    hipLaunchKernelGGL(dep_probe_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+                       static_cast<const int2 *>(table), (uint32_t)(slots - 1), queries, n, chain_len, out, mode,
+                       HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()});
+    return launch_status("dep_probe_kernel");
 }
 
 int xd_gen_hash_kv(uint64_t *keys, uint64_t *vals, uint64_t n, uint64_t seed, void *stream) {

@@ -1,14 +1,23 @@
 // Hash runner: the command line, stdout lines and exit status of the reference's hash
 // benchmark (applications/hash/src/hash_probe_dep.cu:118-385, parsed by
-// applications/hash/run.sh:55-90), on libxdom's uint64 linear-probing table.
+// applications/hash/run.sh:55-90).
 //
-//   xd_hash_run [K Q C L h H runs] [--csv=FILE]     (no positional arguments, or all seven)
+//   xd_hash_run [K Q C L h H runs] [--csv=FILE]                          (reference workload)
+//   xd_hash_run --workload=insert_lookup [K Q C L h H runs] [--csv=FILE] (uint64 table)
 //
+// No positional arguments, or all seven (:119-122). The default workload is the reference's
+// own: K int32 keys with successors in a table of C 8-byte entries, two hot pools of H keys
+// homed on opposite I/O dies and chained into cycles, Q queries of which h percent alternate
+// the hot pools, each following its chain for L dependent probes (xd_dep_*; defaults K =
+// 32000000, Q = 8000000, C = 2^26, L = 4, h = 80, H = 100000, runs = 7 as in :124-130).
+// "Persistent baseline" = XD_MODE_OBLIVIOUS, "Aware" = queries routed on the device to the die
+// that homes their first slot, "Swapped" = to the other die. Correctness as in the reference:
+// the three outputs agree (:345-353); exit 1 otherwise.
+//
+// --workload=insert_lookup: the build's insert + lookup configuration on the uint64 table.
 // K keys (xd_gen_hash_kv, seed 42) are inserted into a table of C slots (C a power of
 // two), then Q lookups run (xd_gen_hash_queries, qseed 4242: even queries hit, odd ones
-// miss). Defaults are the build's benchmark configuration: K = 2^26, Q = 2^26, C = 2^27.
-// L (dependent chain length), h (hot-query percent) and H (hot keys per side) shape the
-// reference's dependent-probe workload and are accepted and echoed only. A timed run is
+// miss). Defaults: K = 2^26, Q = 2^26, C = 2^27; L, h and H are echoed only. A timed run is
 // clear + insert + lookup. "Persistent baseline" = XD_MODE_OBLIVIOUS, "Aware" =
 // XD_MODE_AWARE (keys routed to the die homing their slot, with the table's measured home
 // map), "Swapped" = XD_MODE_ROTATED. Correctness: every mode's found/value output equals
@@ -20,12 +29,111 @@
 
 using namespace runner;
 
+static int dep_probe(const Options &o);
+static int insert_lookup(const Options &o);
+
 int main(int argc, char **argv) {
     Options o(argc, argv);
-    if (o.help || (o.pos.size() != 0 && o.pos.size() != 7)) {
-        fprintf(stderr, "Usage: %s K Q C L h H runs [--csv=FILE]\n", argv[0]);
+    std::string workload = "dep";
+    std::vector<std::string> pos;
+    for (auto &a : o.pos) {
+        if (!a.compare(0, 11, "--workload=")) workload = a.substr(11);
+        else pos.push_back(a);
+    }
+    o.pos = pos;
+    if (o.help || (o.pos.size() != 0 && o.pos.size() != 7) || (workload != "dep" && workload != "insert_lookup")) {
+        fprintf(stderr, "Usage: %s [--workload=dep|insert_lookup] K Q C L h H runs [--csv=FILE]\n", argv[0]);
         return o.help ? 0 : 2;
     }
+    return workload == "dep" ? dep_probe(o) : insert_lookup(o);
+}
+
+static int dep_probe(const Options &o) {
+    const long long K = o.geti(0, 32000000), Q = o.geti(1, 8000000);
+    const unsigned long long C = (unsigned long long)o.geti(2, 1ll << 26);
+    const int L = (int)o.geti(3, 4), h = (int)o.geti(4, 80), H = (int)o.geti(5, 100000);
+    const int runs = (int)o.geti(6, 7);
+    if (K <= 0 || Q <= 0 || K > INT32_MAX || Q > INT32_MAX || C < 2 || (C & (C - 1)) || C > (1ull << 32) ||
+        (unsigned long long)K >= C || L <= 0 || h < 0 || h > 100 || H <= 0 || 2LL * H > K || runs <= 0) {
+        fprintf(stderr, "need 0 < K < C (a power of two), 0 < Q, L > 0, 0 <= h <= 100, 0 < 2H <= K, runs > 0\n");
+        return 2;
+    }
+    const xd_topology_t topo = topology();
+    hipStream_t s;
+    RUN_HIP(hipStreamCreate(&s));
+    const size_t tbytes = (size_t)C * 8;
+    char *raw;
+    RUN_HIP(hipMalloc(&raw, tbytes + (2u << 20)));
+    int32_t *table = reinterpret_cast<int32_t *>(((uintptr_t)raw + (2u << 20) - 1) & ~(uintptr_t)((2u << 20) - 1));
+    HomeMap home(table, tbytes, s);
+    std::vector<uint8_t> attr(xd_home_map_pages(table, tbytes));
+    RUN_HIP(hipMemcpy(attr.data(), home.attr, attr.size(), hipMemcpyDeviceToHost));
+    std::vector<int32_t> keys((size_t)K), nexts((size_t)K), ht(2 * (size_t)C), q((size_t)Q);
+    RUN_XD(xd_dep_make_keys(reinterpret_cast<uint64_t>(table), C, attr.data(), (int32_t)K, H, keys.data(), nexts.data()));
+    RUN_XD(xd_dep_build(ht.data(), C, keys.data(), nexts.data(), (int32_t)K, 42));
+    RUN_XD(xd_dep_queries(q.data(), (int32_t)Q, keys.data(), (int32_t)K, H, h, 4242));
+    RUN_HIP(hipMemcpy(table, ht.data(), tbytes, hipMemcpyHostToDevice));
+    // queries per home die of their first slot (the reference's aware_q0 / aware_q1)
+    long long nq[2] = {0, 0};
+    auto mix32 = [](uint32_t x) {
+        x ^= x >> 16;
+        x *= 0x7feb352du;
+        x ^= x >> 15;
+        x *= 0x846ca68bu;
+        x ^= x >> 16;
+        return x;
+    };
+    const uint64_t tb = reinterpret_cast<uint64_t>(table);
+    for (long long i = 0; i < Q; ++i) {
+        const uint64_t a = tb + (uint64_t)(mix32((uint32_t)q[i]) & (uint32_t)(C - 1)) * 8;
+        nq[((a >> 13) & 1u) ^ attr[(a >> 21) - (tb >> 21)]]++;
+    }
+    int32_t *dq, *dout[3];
+    RUN_HIP(hipMalloc(&dq, (size_t)Q * 4));
+    for (auto &p : dout) RUN_HIP(hipMalloc(&p, (size_t)Q * 4));
+    RUN_HIP(hipMemcpy(dq, q.data(), (size_t)Q * 4, hipMemcpyHostToDevice));
+
+    printf("=== Dependent Hash Probe (XCD domains) ===\n");
+    printf("CONFIG K=%lld Q=%lld C=%llu effective_load=%.6f L=%d h=%d H=%d runs=%d\n\n", K, Q, C, 100.0 * K / C, L, h, H,
+           runs);
+    printf("table=%.1f MiB chunks=%zu hot_chain_set_per_side=%.1f MiB aware_q0=%lld aware_q1=%lld gpu=%s\n\n",
+           tbytes / 1048576.0, tbytes / 8192, H * 8.0 / 1048576.0, nq[0], nq[1], topo.name);
+    auto run = [&](int mode) {
+        return time_ms(s, [&] { RUN_XD(xd_dep_probe(table, C, dq, (uint64_t)Q, L, dout[mode], mode, home.attr, s)); });
+    };
+    for (int mode = 0; mode < 3; ++mode) run(mode);
+    std::vector<int32_t> r0((size_t)Q), r1((size_t)Q), r2((size_t)Q);
+    RUN_HIP(hipMemcpy(r0.data(), dout[0], (size_t)Q * 4, hipMemcpyDeviceToHost));
+    RUN_HIP(hipMemcpy(r1.data(), dout[1], (size_t)Q * 4, hipMemcpyDeviceToHost));
+    RUN_HIP(hipMemcpy(r2.data(), dout[2], (size_t)Q * 4, hipMemcpyDeviceToHost));
+    const bool pass = r0 == r1 && r0 == r2;
+    printf("Correctness: %s\n\n", pass ? "PASS" : "FAIL");
+    double tbm = 0, ta = 0, ts = 0;
+    for (int r = 0; r < runs; ++r) {
+        tbm += run(0);
+        ta += run(1);
+        ts += run(2);
+    }
+    const double b = tbm / runs, a = ta / runs, w = ts / runs;
+    printf("%-28s %8.3f ms\n", "Persistent baseline", b);
+    printf("%-28s %8.3f ms  (speedup %.2fx)\n", "Aware", a, b / a);
+    printf("%-28s %8.3f ms  (speedup %.2fx)\n", "Swapped", w, b / w);
+    printf("mprobes_per_s baseline=%.1f aware=%.1f swapped=%.1f\n", (double)Q * L / (b * 1e3), (double)Q * L / (a * 1e3),
+           (double)Q * L / (w * 1e3));
+    printf("RESULT baseline_ms=%.6f aware_ms=%.6f swapped_ms=%.6f aware_speedup=%.6f swapped_speedup=%.6f pass=%s\n", b, a,
+           w, b / a, b / w, pass ? "PASS" : "FAIL");
+    char row[512];
+    snprintf(row, sizeof row, "%lld,%lld,%llu,%.6f,%d,%d,%d,%.6f,%.6f,%.6f,%.6f,%.6f,%s", K, Q, C, 100.0 * K / C, L, h, H,
+             b, a, w, b / a, b / w, pass ? "PASS" : "FAIL");
+    csv_append(o.csv, "K,Q,C,effective_load,L,h,H,baseline_ms,aware_ms,swapped_ms,aware_speedup,swapped_speedup,pass",
+               row);
+    for (auto p : dout) (void)hipFree(p);
+    (void)hipFree(dq);
+    (void)hipFree(raw);
+    return pass ? 0 : 1;
+}
+
+static int insert_lookup(const Options &o) {
     const uint64_t K = (uint64_t)o.geti(0, 1ll << 26);
     const uint64_t Q = (uint64_t)o.geti(1, 1ll << 26);
     const uint64_t C = (uint64_t)o.geti(2, 1ll << 27);

@@ -48,6 +48,8 @@ _SIGS = {
     "ora_rmat_edge": (None, [I, D, D, D, U64, U64, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "ora_rmat_csr": (I64, [I, I, D, D, D, U64, VP, VP]),
     "ora_bfs": (I64, [VP, VP, C.c_int32, C.c_int32, VP]),
+    "ora_dep_build": (I, [VP, U64, VP, VP, C.c_int32, U64]),
+    "ora_dep_probe": (None, [VP, U64, VP, I64, I, VP]),
 }
 for _n, (_r, _a) in _SIGS.items():
     _f = getattr(lib, _n)
@@ -206,3 +208,23 @@ def bfs(rowptr: np.ndarray, col: np.ndarray, src: int):
     level = np.empty(V, dtype=np.uint32)
     n = int(lib.ora_bfs(_p(rowptr), _p(col) if col.size else None, V, src, _p(level)))
     return level, n
+
+
+def dep_build(slots: int, keys: np.ndarray, nexts: np.ndarray, seed: int) -> np.ndarray:
+    """HASH.cu:226-241: int32 table[slots, 2] = {key, next}, serial shuffled insertion."""
+    keys = np.ascontiguousarray(keys, dtype=np.int32)
+    nexts = np.ascontiguousarray(nexts, dtype=np.int32)
+    t = np.empty(2 * slots, dtype=np.int32)
+    rc = lib.ora_dep_build(_p(t), slots, _p(keys), _p(nexts), keys.size, seed)
+    if rc:
+        raise ValueError("dep_build failed")
+    return t
+
+
+def dep_probe(table: np.ndarray, slots: int, queries: np.ndarray, chain_len: int) -> np.ndarray:
+    """HASH.cu:46-83: out[i] = (sum of found slots, -1 per miss) ^ final key."""
+    queries = np.ascontiguousarray(queries, dtype=np.int32)
+    out = np.empty(queries.size, dtype=np.int32)
+    lib.ora_dep_probe(_p(np.ascontiguousarray(table, dtype=np.int32)), slots, _p(queries), queries.size, chain_len,
+                      _p(out))
+    return out

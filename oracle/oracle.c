@@ -467,3 +467,66 @@ int64_t ora_bfs(const int32_t *rowptr, const int32_t *col, int32_t V, int32_t sr
     free(q);
     return tail;
 }
+
+/* ------------------------------------------------------------------------------------ */
+/* Dependent-probe hash (HASH.cu:29-83, 226-241)                                          */
+/* ------------------------------------------------------------------------------------ */
+int ora_dep_build(int32_t *table, uint64_t slots, const int32_t *keys, const int32_t *nexts, int32_t K,
+                  uint64_t seed) {
+    if ((uint64_t)K >= slots) return -1;
+    const uint32_t mask = (uint32_t)(slots - 1);
+    for (uint64_t s = 0; s < slots; ++s) {
+        table[2 * s] = -1;
+        table[2 * s + 1] = 0;
+    }
+    int32_t *perm = (int32_t *)malloc(sizeof(int32_t) * (size_t)K);
+    if (!perm) return -2;
+    for (int32_t i = 0; i < K; ++i) perm[i] = i;
+    for (int64_t i = (int64_t)K - 1; i > 0; --i) {
+        const int64_t j = (int64_t)(ora_splitmix64(seed, (uint64_t)i) % (uint64_t)(i + 1));
+        const int32_t t = perm[i];
+        perm[i] = perm[j];
+        perm[j] = t;
+    }
+    for (int32_t k = 0; k < K; ++k) {
+        const int32_t p = perm[k];
+        uint32_t slot = ora_mix32((uint32_t)keys[p]) & mask;
+        while (table[2 * (size_t)slot] != -1) slot = (slot + 1) & mask;
+        table[2 * (size_t)slot] = keys[p];
+        table[2 * (size_t)slot + 1] = nexts[p];
+    }
+    free(perm);
+    return 0;
+}
+
+static int32_t dep_probe_one(const int32_t *table, uint32_t mask, int32_t key, int32_t *next_key) {
+    uint32_t slot = ora_mix32((uint32_t)key) & mask;
+    int32_t fkey = -1, fnext = key;
+    for (uint64_t step = 0; step <= mask; ++step) {
+        const int32_t ek = table[2 * (size_t)slot], en = table[2 * (size_t)slot + 1];
+        if (ek == key) {
+            fkey = ek;
+            fnext = en;
+            break;
+        }
+        if (ek == -1) break;
+        slot = (slot + 1) & mask;
+    }
+    *next_key = fnext;
+    return fkey == key ? (int32_t)slot : -1;
+}
+
+void ora_dep_probe(const int32_t *table, uint64_t slots, const int32_t *queries, int64_t n, int chain_len,
+                   int32_t *out) {
+    const uint32_t mask = (uint32_t)(slots - 1);
+    for (int64_t i = 0; i < n; ++i) {
+        int32_t key = queries[i];
+        uint32_t acc = 0;
+        for (int it = 0; it < chain_len; ++it) {
+            int32_t nk;
+            acc += (uint32_t)dep_probe_one(table, mask, key, &nk);
+            key = nk;
+        }
+        out[i] = (int32_t)(acc ^ (uint32_t)key);
+    }
+}

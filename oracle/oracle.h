@@ -62,4 +62,13 @@ int64_t ora_rmat_csr(int scale, int edge_factor, double a, double b, double c, u
 /* Serial FIFO-queue BFS; returns the number of reached vertices. */
 int64_t ora_bfs(const int32_t *rowptr, const int32_t *col, int32_t V, int32_t src, uint32_t *level);
 
+/* The reference's dependent-probe workload (applications/hash/src/hash_probe_dep.cu).
+ * ora_dep_build: table[2*slots] {key, next}, EMPTY -1, serial insertion (HASH.cu:232-241) in
+ * the order of a Fisher-Yates shuffle (i = K-1 .. 1, j = splitmix64(seed, i) mod (i + 1)).
+ * ora_dep_probe: probe_dep_base (HASH.cu:66-83) with probe_chain_one (:46-64), int wraps. */
+int ora_dep_build(int32_t *table, uint64_t slots, const int32_t *keys, const int32_t *nexts, int32_t K,
+                  uint64_t seed);
+void ora_dep_probe(const int32_t *table, uint64_t slots, const int32_t *queries, int64_t n, int chain_len,
+                   int32_t *out);
+
 #endif

@@ -56,15 +56,20 @@ def test_hist_runner(tmp_path):
     assert (tmp_path / "h.csv").read_text().splitlines()[1].split(",")[18] == "PASS"
 
 
-def test_hash_runner(tmp_path):
-    rc, out, err = run("xd_hash_run", 1 << 20, 1 << 20, 1 << 21, 1, 50, 0, 2, csv=tmp_path / "x.csv")
+@pytest.mark.parametrize("workload", ["dep", "insert_lookup"])
+def test_hash_runner(tmp_path, workload):
+    args = [1 << 20, 1 << 20, 1 << 21, 4, 80, 10000, 2]
+    if workload == "insert_lookup":
+        args = ["--workload=insert_lookup", 1 << 20, 1 << 20, 1 << 21, 1, 50, 0, 2]
+    rc, out, err = run("xd_hash_run", *args, csv=tmp_path / "x.csv")
     assert rc == 0, out + err
     assert "Correctness: PASS" in out
     res = next(l for l in out.splitlines() if l.startswith("RESULT "))
-    kv = dict(t.split("=") for t in res.split()[1:])
+    kv = dict(t.split("=") for t in res.split()[1:])  # applications/hash/run.sh:62-66
     assert kv["pass"] == "PASS"
     for key in ("baseline_ms", "aware_ms", "swapped_ms", "aware_speedup", "swapped_speedup"):
         assert float(kv[key]) > 0
+    assert (tmp_path / "x.csv").read_text().splitlines()[0].startswith("K,Q,C,effective_load,L,h,H,baseline_ms")
 
 
 def test_bfs_runner(tmp_path):

@@ -306,3 +306,69 @@ def test_derive_active_bits_rule():
     assert derive_active_bits([3, 5, 9], [3, 9, 5]) == [False, False, True]
     with pytest.raises(ValueError):
         derive_active_bits([1, 2], [1, 2])
+
+
+def test_dep_oracle_small_brute_force():
+    # dependent-probe oracle against a Python restatement on a tiny table, including misses
+    # and a full chain cycle
+    rng = np.random.default_rng(5)
+    slots, K = 64, 40
+    keys = (2 * np.arange(1, K + 1) + 1).astype(np.int32)
+    nexts = np.roll(keys, -1)
+    t = ora.dep_build(slots, keys, nexts, 7)
+    tk, tn = t[0::2], t[1::2]
+    assert sorted(tk[tk != -1].tolist()) == sorted(keys.tolist())
+
+    def probe_one(key):
+        slot = ora.mix32(key & 0xFFFFFFFF) & (slots - 1)
+        for _ in range(slots):
+            if tk[slot] == key:
+                return slot, int(tn[slot])
+            if tk[slot] == -1:
+                break
+            slot = (slot + 1) % slots
+        return -1, key
+
+    q = np.concatenate([rng.choice(keys, 30), np.array([2, 4, 1000], dtype=np.int32)]).astype(np.int32)
+    for L in (1, 3, 7):
+        want = []
+        for key in q.tolist():
+            acc = 0
+            for _ in range(L):
+                s, key = probe_one(key)
+                acc = (acc + s) & 0xFFFFFFFF
+            want.append(np.array([acc ^ (key & 0xFFFFFFFF)], dtype=np.uint32).view(np.int32)[0])
+        np.testing.assert_array_equal(ora.dep_probe(t, slots, q, L), np.array(want, dtype=np.int32))
+
+
+def test_dep_product_build_matches_oracle():
+    # the library's host build (shuffle + serial insertion) equals the oracle's restatement
+    import ctypes as C
+    from l2domain_amd import _lib
+    slots, K = 1 << 12, 3000
+    keys = (2 * np.arange(K) + 1).astype(np.int32)
+    nexts = np.roll(keys, -7)
+    t = np.empty(2 * slots, dtype=np.int32)
+    assert _lib.lib.xd_dep_build(t.ctypes.data, slots, keys.ctypes.data, nexts.ctypes.data, K, 42) == 0
+    np.testing.assert_array_equal(t, ora.dep_build(slots, keys, nexts, 42))
+
+
+def test_dep_make_keys_pools_and_queries():
+    from l2domain_amd import _lib
+    slots, K, H = 1 << 16, 20000, 3000
+    base = 0x7f0000000000  # any 2 MiB-aligned address; homes from the address mask
+    keys = np.empty(K, dtype=np.int32)
+    nexts = np.empty(K, dtype=np.int32)
+    assert _lib.lib.xd_dep_make_keys(base, slots, None, K, H, keys.ctypes.data, nexts.ctypes.data) == 0
+    assert len(set(keys.tolist())) == K and np.all(keys % 2 == 1)
+    mask = int(_lib.lib.xd_home_mask())
+    side = lambda k: bin((base + (ora.mix32(int(k)) & (slots - 1)) * 8) & mask).count("1") & 1
+    assert all(side(k) == 0 for k in keys[:H]) and all(side(k) == 1 for k in keys[H:2 * H])
+    np.testing.assert_array_equal(nexts[:H], np.roll(keys[:H], -1))          # hot pools are cycles
+    np.testing.assert_array_equal(nexts[H:2 * H], np.roll(keys[H:2 * H], -1))
+    np.testing.assert_array_equal(nexts[2 * H:], keys[2 * H:])              # cold keys loop on themselves
+    q = np.empty(1000, dtype=np.int32)
+    assert _lib.lib.xd_dep_queries(q.ctypes.data, 1000, keys.ctypes.data, K, H, 80, 9) == 0
+    hot0, hot1 = set(keys[:H].tolist()), set(keys[H:2 * H].tolist())
+    assert all((x in hot1) if i % 2 else (x in hot0) for i, x in enumerate(q[:800].tolist()))
+    assert set(q.tolist()) <= set(keys.tolist())

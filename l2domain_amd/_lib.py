@@ -9,6 +9,14 @@ import ctypes as C
 import os
 from pathlib import Path
 
+# torch ships its own HIP and HSA runtime libraries. In a process that uses both, torch has
+# to be loaded before libxdom.so (which links /opt/rocm's): loaded the other way round, the
+# library's HIP calls report hipErrorNoDevice once torch has initialised the device.
+try:
+    import torch  # noqa: F401
+except ImportError:  # pragma: no cover - the library itself does not need torch
+    pass
+
 PKG = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("XDOM_LIB", PKG / "libxdom.so"))
 

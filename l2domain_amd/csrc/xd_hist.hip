@@ -18,8 +18,11 @@
 //   3. count: one workgroup per item keeps a 128 KB LDS histogram of its bucket, adds each
 //      key with a ds_add (the wave's most common key is peeled into one add), and writes
 //      the LDS histogram to its partial slot;
-//   4. merge: counts = sum of the bucket's partial slots; XCD-aware mode merges on the XCD
-//      that wrote the partials, so they are read back from that XCD's L2.
+//   4. merge: counts = sum of the bucket's partial slots. XCD-aware mode fuses the merge
+//      into the count pass: the last count workgroup of a bucket to finish (a ticket per
+//      bucket) sums the bucket's slots, which its own XCD wrote and still holds in L2; the
+//      merge kernel then only writes the empty buckets. Oblivious and rotated run the merge
+//      kernel over every bucket.
 #include <hip/hip_runtime.h>
 
 #include "xd_common.hpp"

@@ -9,7 +9,7 @@ steps timed with HIP events on the stream the kernels are launched on. Prints ON
 `value` is the XCD-aware variant's throughput; the oblivious and rotated variants are
 timed over the same K steps and reported beside it with the aware/oblivious speedup.
 Unless --only is given, every other configuration (GEMV fp32 and fp16 warm and cold, hash,
-BFS) is measured the same way, with at most 50 timed steps, under "extras".
+the reference's dependent probe and byte histogram, BFS) is measured the same way, with at most 50 timed steps, under "extras".
 """
 from __future__ import annotations
 
@@ -308,6 +308,72 @@ class Hash:
                 "sample": "2^23 serial inserts into 2^24 slots + 2^23 lookups (oracle, HASH.cu:46-64,226-241)"}
 
 
+class Hist256:
+    """The reference's own histogram workload (histogram256_sideaware.cu): data_mb = 512 (the
+    paper preset's largest, applications/histogram/run.sh:16) of words[i] = mix32(i), every
+    byte counted into 256 bins. A step = one xd_hist256_u32bytes call (count + fused merge)."""
+    name = "hist256_bytes_512MiB_mix32"
+    unit = "GB/s"
+    dtype = "u8"
+    dominant = "hist256"
+    single_kernel = True
+
+    def __init__(self, data_mb=512):
+        import numpy as np
+        import torch
+        from l2domain_amd import gen
+        from l2domain_amd.domain import home_map
+        from l2domain_amd.histogram import ByteHistogram
+        self.n = data_mb * (1 << 20) // 4
+        self.data_mb = data_mb
+        self.host = gen.mix32_words(self.n)
+        self.words = torch.from_numpy(self.host.view(np.int32)).cuda()
+        self.home = home_map(self.words.view(torch.uint8))
+        self.bh = ByteHistogram()
+        self.counts = torch.empty(256, dtype=torch.int32, device="cuda")
+        self.bytes = 4 * self.n + 4 * 256
+
+    def step(self, mode):
+        self.bh(self.words, self.counts, mode=mode, home_attr=self.home)
+
+    def throughput(self, sec_per_step):
+        return self.bytes / sec_per_step / 1e9
+
+    def verify(self):
+        import numpy as np
+        import oracle as ora
+        ref = ora.hist256_bytes(self.host, nthreads=_cpu_threads())
+        ok = True
+        for mode in MODES:
+            self.step(mode)
+            ok = ok and bool(np.array_equal(self.counts.cpu().numpy().view(np.uint32), ref))
+        return ok
+
+    def roofline(self, sec_per_launch):
+        achieved = self.bytes / sec_per_launch / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "hist256_kernel",
+                "algorithmic_bytes_per_launch": self.bytes}
+
+    def config(self):
+        return {"workload": self.name, "data_mb": self.data_mb, "words": self.n, "bins": 256,
+                "data": "words[i] = mix32(i) (HIST.cu:331-340)"}
+
+    def cpu_baseline(self):
+        import oracle as ora
+        nt = _cpu_threads()
+        sample = self.host[: 1 << 26]
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 5.0:
+            ora.hist256_bytes(sample, nthreads=nt)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(4 * sample.size / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+                "sample": f"{reps} x 2^26 words of the same data (oracle byte-counting loop, HIST.cu:279-288, "
+                          f"{nt} threads with private histograms)"}
+
+
 class HashDep:
     """The reference's own hash workload (hash_probe_dep.cu, defaults :124-130): K = 32000000
     int32 keys with successors in 2^26 8-byte entries, two hot pools of 100000 keys homed on
@@ -438,6 +504,7 @@ WORKLOADS = {
     "bfs": Bfs,
     "hash": Hash,
     "hash_dep": HashDep,
+    "hist256": Hist256,
     "gemv_f32": GemvF32,
     "gemv_f16_up": lambda: GemvF16(14336, 4096),
     "gemv_f16_down": lambda: GemvF16(4096, 14336),
@@ -446,7 +513,7 @@ DEFAULT_WORKLOAD = "hist"
 # every other BASELINE config, reported under "extras" of the same JSON line
 EXTRAS = (("gemv_f32", False), ("gemv_f32", True), ("gemv_f16_up", False), ("gemv_f16_up", True),
           ("gemv_f16_down", False), ("gemv_f16_down", True), ("hash", False), ("hash_dep", False),
-          ("bfs", False))
+          ("bfs", False), ("hist256", True), ("hist256", False))
 
 
 # ---------------------------------------------------------------------------------------

@@ -209,6 +209,22 @@ size_t xd_hist_workspace_size(size_t n, uint32_t num_bins);
 int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int mode,
                 void *workspace, size_t workspace_bytes, void *stream);
 
+/* Workspace bytes of xd_hist256_u32bytes (independent of n; about 520 KB). Zero-filled once
+ * when allocated; every call leaves its tickets zeroed again. Calls sharing one workspace
+ * must not overlap. */
+size_t xd_hist256_workspace_size(void);
+
+/* The reference's own histogram: 256 byte-bins, every byte of every word counted,
+ * counts[v] = #{(i, k) : (words[i] >> 8k) & 0xff == v}; all 256 counts are written.
+ * words 16-byte aligned, n < 2^30. Replaces add_word / histogram256_chunked_kernel /
+ * histogram256_persistent_kernel / merge_histogram256_kernel
+ * (applications/histogram/src/histogram256_sideaware.cu:20-25, 51-157) with the near/far
+ * chunk lists of :227-277. Modes: XD_MODE_OBLIVIOUS reads every 8 KiB chunk from any XCD;
+ * XD_MODE_AWARE has each I/O die read only the chunks it homes (home_attr: xd_home_map of
+ * words, or NULL for the address-mask prediction); XD_MODE_ROTATED only the far chunks. */
+int xd_hist256_u32bytes(const uint32_t *words, size_t n, uint32_t *counts, int mode, const uint8_t *home_attr,
+                        void *workspace, size_t workspace_bytes, void *stream);
+
 /* ------------------------------------------------------------------------------------ */
 /* Hash table: open addressing, linear probing, uint64 keys and values                   */
 /* ------------------------------------------------------------------------------------ */
@@ -328,6 +344,18 @@ int xd_gen_uniform_f32(float *out, size_t n, uint64_t seed);
 
 /* out[i] = binary16(RNE) of mean + stddev * N(0,1), Box-Muller over xd_rand64(seed, .). */
 int xd_gen_normal_f16(uint16_t *out, size_t n, double mean, double stddev, uint64_t seed);
+
+/* The reference's mix32-based inputs. mix32 is the lowbias32 finalizer of
+ * applications/gemv/src/gemv_k1024_persistent_subwarp.cu:56-63.
+ * xd_gen_mix32_words: out[i] = mix32((uint32_t)i ^ seed); seed 0 gives the histogram data
+ * of applications/histogram/src/histogram256_sideaware.cu:331-340. */
+int xd_gen_mix32_words(uint32_t *out, size_t n, uint32_t seed);
+
+/* GEMV init_data (gemv_k1024_persistent_subwarp.cu:118-139): with h = mix32((uint32_t)i ^
+ * seed), out[i] = (float)(h & 0xff) / 255.0f - 0.5f when modulus == 0, else
+ * (float)((int32_t)(h % modulus) - offset) (the INTEGER_FLOAT_INPUTS variant: A uses
+ * modulus 17 / offset 8 with seed, x modulus 7 / offset 3 with seed + 0x9e37). */
+int xd_gen_mix32_f32(float *out, size_t n, uint32_t seed, uint32_t modulus, int32_t offset);
 
 /* Zipf(s) over num_bins ranks as 64-bit inverse-CDF thresholds (host, fp64):
  * out[k] = floor(2^64 * sum_{r<=k} (r+1)^-s / H), out[num_bins-1] = 2^64-1. */

@@ -87,6 +87,8 @@ SIGNATURES: dict[str, tuple] = {
     "xd_gemv_f16f32": (I, [VP, VP, VP, I, I, I, VP, VP, SZ, VP]),
     "xd_hist_workspace_size": (SZ, [SZ, U32]),
     "xd_hist_u32": (I, [VP, SZ, VP, U32, I, VP, SZ, VP]),
+    "xd_hist256_workspace_size": (SZ, []),
+    "xd_hist256_u32bytes": (I, [VP, SZ, VP, I, VP, VP, SZ, VP]),
     "xd_hash_table_bytes": (SZ, [U64]),
     "xd_hash_init": (I, [VP, U64, VP]),
     "xd_hash_insert_u64": (I, [VP, U64, VP, VP, U64, I, VP, VP, VP]),
@@ -104,6 +106,8 @@ SIGNATURES: dict[str, tuple] = {
     "xd_rand64": (U64, [U64, U64]),
     "xd_gen_uniform_f32": (I, [VP, SZ, U64]),
     "xd_gen_normal_f16": (I, [VP, SZ, D, D, U64]),
+    "xd_gen_mix32_words": (I, [VP, SZ, U32]),
+    "xd_gen_mix32_f32": (I, [VP, SZ, U32, U32, C.c_int32]),
     "xd_zipf_thresholds": (I, [VP, U32, D]),
     "xd_gen_zipf_keys": (I, [VP, SZ, VP, U32, U64, I, VP]),
     "xd_rmat_edge": (I, [I, D, D, D, U64, U64, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),

@@ -78,10 +78,13 @@ def build_runners(jobs: int = 8) -> list[Path]:
         return []
     BIN.mkdir(exist_ok=True)
 
+    # the vendor-library comparison runner also links rocBLAS (timed for comparison only)
+    extra_libs = {"xd_gemv_vendor_run": ["-L/opt/rocm/lib", "-lrocblas"]}
+
     def one(src: Path) -> Path:
         exe = BIN / src.stem
-        _run([HIPCC, "-O2", "-std=c++17", "-pthread", f"-I{INCLUDE}", f"-I{RUNNERS}", str(src),
-              "-o", str(exe), f"-L{PKG}", "-lxdom", f"-Wl,-rpath,$ORIGIN/.."])
+        _run([HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-pthread", f"-I{INCLUDE}", f"-I{RUNNERS}", str(src),
+              "-o", str(exe), f"-L{PKG}", "-lxdom", *extra_libs.get(src.stem, []), f"-Wl,-rpath,$ORIGIN/.."])
         return exe
 
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:

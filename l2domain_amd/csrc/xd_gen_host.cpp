@@ -27,6 +27,16 @@ inline uint64_t splitmix64_mix(uint64_t z) {
 
 inline uint64_t rand64(uint64_t seed, uint64_t index) { return splitmix64_mix(seed + (index + 1) * kGolden); }
 
+// lowbias32, the reference's integer finalizer (GEMV.cu:56-63)
+inline uint32_t mix32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
 // binary16 bit pattern nearest to d (round to nearest, ties to even).
 uint16_t f64_to_f16_rne(double d) {
     uint64_t bits;
@@ -109,6 +119,26 @@ int xd_gen_normal_f16(uint16_t *out, size_t n, double mean, double stddev, uint6
             double z1 = r * sin(two_pi * u2);
             out[2 * j] = f64_to_f16_rne(mean + stddev * z0);
             if (2 * j + 1 < n) out[2 * j + 1] = f64_to_f16_rne(mean + stddev * z1);
+        }
+    });
+    return XD_OK;
+}
+
+int xd_gen_mix32_words(uint32_t *out, size_t n, uint32_t seed) {
+    if (out == nullptr && n != 0) return XD_ERR_INVALID_ARG;
+    parallel_for(n, [&](size_t b, size_t e) {
+        for (size_t i = b; i < e; ++i) out[i] = mix32((uint32_t)i ^ seed);
+    });
+    return XD_OK;
+}
+
+int xd_gen_mix32_f32(float *out, size_t n, uint32_t seed, uint32_t modulus, int32_t offset) {
+    if (out == nullptr && n != 0) return XD_ERR_INVALID_ARG;
+    parallel_for(n, [&](size_t b, size_t e) {
+        for (size_t i = b; i < e; ++i) {
+            const uint32_t h = mix32((uint32_t)i ^ seed);
+            // binary32 division and subtraction, each rounded to nearest (no excess precision)
+            out[i] = modulus ? (float)((int32_t)(h % modulus) - offset) : (float)(h & 0xffu) / 255.0f - 0.5f;
         }
     });
     return XD_OK;

@@ -1,0 +1,264 @@
+// 256-bin byte histogram of uint32 words: counts[v] = #{(i, k) : byte k of words[i] == v},
+// the reference's own histogram workload.
+//
+// Reference: applications/histogram/src/histogram256_sideaware.cu
+//   add_word (20-25): the four bytes of a word, one shared-memory atomicAdd each, into
+//     per-warp 256-bin sub-histograms; histogram256_chunked_kernel (51-85) walks a list of
+//     4 KiB chunks; histogram256_persistent_kernel (87-134) gives the SMs of each L2 side
+//     the chunks homed on that side (near/far lists, 227-277); merge_histogram256_kernel
+//     (136-157) sums the per-block partials; the data is words[i] = mix32(i) (331-340).
+//
+// MI355X design.
+//   counting: one 64 KiB LDS histogram per workgroup laid out as 256 bins x 64 columns;
+//     lane l of every wave adds into column l, so the 64 adds of one ds_add instruction sit
+//     in 64 different banks whatever the bytes are (no bank conflict, no same-address
+//     collision inside an instruction).
+//   routing: memory is homed per 8 KiB chunk on one of the two I/O dies; the two chunks of
+//     an aligned 16 KiB pair lie in one 2 MiB page and differ in address bit 13, so each
+//     die homes one of them. Oblivious: workgroup b reads both chunks of pairs b, b + grid,
+//     ... XCD-aware: the workgroups of a die (XCDs 0-3 or 4-7) take pairs rank, rank +
+//     grid/2, ... and read only the chunk their own die homes, so every byte comes from the
+//     near die; rotated reads only the far chunk. A pipeline slot holds two chunks (one pair
+//     oblivious, two pairs in the home modes) and a workgroup keeps three slots in flight
+//     while it counts one. The page map is staged in LDS first: a home lookup from global
+//     memory would make the next load wait for every load in flight. Without a page map the
+//     address mask decides, rounded to pairs (its bits below 14 are taken as bit 13 alone).
+//     Every load of the main loop is issued unconditionally (indices clamped into the data,
+//     out-of-range vectors counted as empty): a load under a branch makes the compiler wait
+//     for all loads in flight where the branches join. The last n mod 4 words are counted
+//     separately by workgroup 0.
+//   merge (fused, no fences): each workgroup adds its 256 sums, two bins per 64-bit word, to
+//     the accumulators of its group b mod 8 with returning memory-side atomics, then takes
+//     the group's ticket; the last of a group takes the final ticket, and the last of those
+//     reads and clears the accumulators with atomic exchanges and writes counts. Every
+//     atomic has returned before the ticket after it is issued, so the last taker sees all
+//     the sums. A 32-bit half never carries: a bin's total is at most 4n < 2^32. Tickets and
+//     accumulators are left zeroed.
+#include <hip/hip_runtime.h>
+
+#include "xd_common.hpp"
+
+namespace xd {
+
+constexpr int kH8Bins = 256;
+constexpr int kH8Pairs = kH8Bins / 2;  // 64-bit accumulators, two bins each
+constexpr int kH8Threads = 512;
+constexpr int kH8Ahead = 3;          // slots loaded ahead of the one being counted
+constexpr int kH8MaxGrid = 512;      // two workgroups per CU (64 KiB of LDS each)
+constexpr uint64_t kH8Chunk = 8192;  // the unit of memory home; 512 x 16 B = one vector per thread
+constexpr int kH8MaxPages = 2056;    // n < 2^30 words spans at most 2049 pages of 2 MiB
+
+struct H8Layout {
+    size_t acc, sync, total;
+};
+
+static H8Layout h8_layout() {
+    H8Layout L;
+    L.acc = 0;
+    L.sync = L.acc + (size_t)kNumXcd * kH8Pairs * 8;
+    L.total = L.sync + 256;  // 8 group tickets + 1 final ticket
+    return L;
+}
+
+__device__ __forceinline__ void h8_add_word(uint32_t *h, uint32_t w, uint32_t lane) {
+    atomicAdd(&h[((w & 0xffu) << 6) | lane], 1u);
+    atomicAdd(&h[(((w >> 8) & 0xffu) << 6) | lane], 1u);
+    atomicAdd(&h[(((w >> 16) & 0xffu) << 6) | lane], 1u);
+    atomicAdd(&h[((w >> 24) << 6) | lane], 1u);
+}
+
+__device__ __forceinline__ void h8_add_vec(uint32_t *h, uint4 v, uint32_t nv, uint32_t lane) {
+    if (nv == 4u) {
+        h8_add_word(h, v.x, lane);
+        h8_add_word(h, v.y, lane);
+        h8_add_word(h, v.z, lane);
+        h8_add_word(h, v.w, lane);
+    } else {
+        if (nv > 0u) h8_add_word(h, v.x, lane);
+        if (nv > 1u) h8_add_word(h, v.y, lane);
+        if (nv > 2u) h8_add_word(h, v.z, lane);
+    }
+}
+
+// This thread's 16 bytes of chunk c (absolute chunk index = address / 8 KiB): words4 holds
+// the nvec full vectors of the data, which start at address wbeg (16-byte aligned). ok = the
+// vector lies inside them; otherwise vector 0 is loaded (the load stays unconditional) and
+// must not be counted. Indexing from the kernel's pointer argument keeps the load in the
+// global address space (a flat load would also count against the LDS wait counter).
+__device__ __forceinline__ uint4 h8_load(const uint4 *__restrict__ words4, uint64_t c, uint64_t wbeg, uint64_t nvec,
+                                         int tid, bool &ok) {
+    const uint64_t a = c * kH8Chunk + (uint64_t)tid * 16u;
+    const uint64_t i = (a - wbeg) / 16u;  // wraps to a huge value below wbeg
+    ok = a >= wbeg && i < nvec;
+    return words4[ok ? i : 0];
+}
+
+__global__ void __launch_bounds__(kH8Threads)
+hist256_kernel(const uint32_t *__restrict__ words, uint64_t n, uint64_t pair0, uint64_t npairs, int mode,
+               HomeMap home, unsigned long long *__restrict__ acc, uint32_t *__restrict__ sync,
+               uint32_t *__restrict__ counts) {
+    __shared__ __attribute__((aligned(16))) uint32_t h[kH8Bins * kWave];
+    __shared__ uint8_t lattr[kH8MaxPages];
+    __shared__ uint32_t s_last;
+    const int tid = (int)threadIdx.x;
+    const uint32_t lane = (uint32_t)tid & (kWave - 1);
+    const int b = (int)blockIdx.x, grid = (int)gridDim.x;
+    const uint64_t wbeg = reinterpret_cast<uint64_t>(words);
+    const uint64_t nvec = n / 4;
+    const uint4 *words4 = reinterpret_cast<const uint4 *>(words);
+    uint4 *h4 = reinterpret_cast<uint4 *>(h);
+    for (int i = tid; i < kH8Bins * kWave / 4; i += kH8Threads) h4[i] = make_uint4(0, 0, 0, 0);
+    const bool routed = mode != XD_MODE_OBLIVIOUS;
+    if (routed && home.attr != nullptr && npairs > 0) {
+        const uint64_t npages = (wbeg + 16 * nvec - 1) / kHomePage - home.page0 + 1;
+        for (uint64_t p = (uint64_t)tid; p < npages; p += kH8Threads) lattr[p] = home.attr[p];
+    }
+    __syncthreads();
+
+    uint64_t first, step;  // this workgroup's pairs: first + j * step, j < npm
+    uint32_t want = 0;
+    if (!routed) {
+        first = (uint64_t)b;
+        step = (uint64_t)grid;
+    } else {
+        first = (uint64_t)((b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2)));
+        step = (uint64_t)(grid / 2);
+        const uint32_t die = wg_die(b);
+        want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
+    }
+    const uint64_t npm = first < npairs ? (npairs - first + step - 1) / step : 0;
+    const uint64_t nslots = routed ? (npm + 1) / 2 : npm;
+
+    // the chunk of pair P (absolute) homed on the wanted die: the even chunk's home is the
+    // page attribute (its bit 13 is 0), and the odd chunk is homed on the other die
+    auto wanted = [&](uint64_t P) -> uint64_t {
+        const uint64_t a = 2 * P * kH8Chunk;
+        const uint32_t h0 = home.attr ? (uint32_t)lattr[a / kHomePage - home.page0] : home_of(a, home.mask & ~0x3fffull);
+        return 2 * P + (h0 ^ want);
+    };
+    // slot k: vectors a and c, n = a valid | c valid << 1
+    auto load_slot = [&](uint64_t k, uint4 &a, uint4 &c, uint32_t &nv) {
+        uint64_t ca, cc;
+        bool okc = true;
+        if (!routed) {
+            const uint64_t P = pair0 + first + k * step;
+            ca = 2 * P;
+            cc = 2 * P + 1;
+        } else {
+            const uint64_t Pa = pair0 + first + 2 * k * step;
+            okc = 2 * k + 1 < npm;
+            ca = wanted(Pa);
+            cc = wanted(okc ? Pa + step : Pa);
+        }
+        bool oa, oc;
+        a = h8_load(words4, ca, wbeg, nvec, tid, oa);
+        c = h8_load(words4, cc, wbeg, nvec, tid, oc);
+        nv = (oa ? 1u : 0u) | ((oc && okc) ? 2u : 0u);
+    };
+    auto count = [&](const uint4 &a, const uint4 &c, uint32_t nv) {
+        if (nv & 1u) h8_add_vec(h, a, 4u, lane);
+        if (nv & 2u) h8_add_vec(h, c, 4u, lane);
+    };
+
+    if (nslots > 0 && nvec > 0) {
+        uint4 ra[kH8Ahead], rc[kH8Ahead];
+        uint32_t rn[kH8Ahead];
+#pragma unroll
+        for (int j = 0; j < kH8Ahead; ++j)
+            load_slot(std::min<uint64_t>((uint64_t)j, nslots - 1), ra[j], rc[j], rn[j]);
+        uint64_t k0 = 0;
+        for (; k0 + kH8Ahead <= nslots; k0 += kH8Ahead) {
+#pragma unroll
+            for (int j = 0; j < kH8Ahead; ++j) {
+                const uint4 a = ra[j], c = rc[j];
+                const uint32_t nv = rn[j];
+                load_slot(std::min<uint64_t>(k0 + j + kH8Ahead, nslots - 1), ra[j], rc[j], rn[j]);
+                count(a, c, nv);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kH8Ahead; ++j)
+            if (k0 + (uint64_t)j < nslots) count(ra[j], rc[j], rn[j]);
+    }
+    if (b == 0 && (uint64_t)tid < n - 4 * nvec) h8_add_word(h, words[4 * nvec + (uint64_t)tid], lane);
+    __syncthreads();
+
+    // This workgroup's sums of bins 2t and 2t + 1 (thread t < 128) over the 64 columns,
+    // starting at column t mod 64 so that the lanes of a wave read 64 different banks.
+    const int g = b % kNumXcd;
+    if (tid < kH8Pairs) {
+        uint32_t s0 = 0, s1 = 0;
+        for (int col = 0; col < kWave; ++col) {
+            const int cc = (col + tid) & (kWave - 1);
+            s0 += h[(2 * tid) * kWave + cc];
+            s1 += h[(2 * tid + 1) * kWave + cc];
+        }
+        const unsigned long long r =
+            atomicAdd(&acc[g * kH8Pairs + tid], (unsigned long long)s0 | ((unsigned long long)s1 << 32));
+        asm volatile("" ::"v"(r));  // a returning atomic: performed before the ticket is taken
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const int per_group = grid / kNumXcd;
+        uint32_t last = 0;
+        if (atomicAdd(&sync[g], 1u) == (uint32_t)(per_group - 1)) {
+            atomicExch(&sync[g], 0u);
+            if (atomicAdd(&sync[kNumXcd], 1u) == (uint32_t)(kNumXcd - 1)) {
+                atomicExch(&sync[kNumXcd], 0u);
+                last = 1;
+            }
+        }
+        s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (tid < kH8Pairs) {
+        unsigned long long tot = 0;
+        for (int x = 0; x < kNumXcd; ++x) tot += atomicExch(&acc[x * kH8Pairs + tid], 0ull);
+        counts[2 * tid] = (uint32_t)tot;
+        counts[2 * tid + 1] = (uint32_t)(tot >> 32);
+    }
+}
+
+}  // namespace xd
+
+using namespace xd;
+
+extern "C" {
+
+size_t xd_hist256_workspace_size(void) { return h8_layout().total; }
+
+int xd_hist256_u32bytes(const uint32_t *words, size_t n, uint32_t *counts, int mode, const uint8_t *home_attr,
+                        void *workspace, size_t workspace_bytes, void *stream) {
+    XD_REQUIRE(counts != nullptr && (reinterpret_cast<uintptr_t>(counts) & 3u) == 0,
+               "xd_hist256_u32bytes: counts is NULL or not 4-byte aligned");
+    XD_REQUIRE(n == 0 || (words != nullptr && aligned16(words)),
+               "xd_hist256_u32bytes: words is NULL or not 16-byte aligned");
+    XD_REQUIRE(n < (1ull << 30), "xd_hist256_u32bytes: n must be < 2^30 (4n u32 counts)");
+    XD_REQUIRE(n == 0 || (4ull * n + (reinterpret_cast<uintptr_t>(words) % kHomePage) - 1) / kHomePage < (uint64_t)kH8MaxPages,
+               "xd_hist256_u32bytes: the words span too many 2 MiB pages");
+    XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_hist256_u32bytes: bad mode");
+    const H8Layout L = h8_layout();
+    if (workspace == nullptr || workspace_bytes < L.total || !aligned16(workspace))
+        return fail(XD_ERR_WORKSPACE,
+                    "xd_hist256_u32bytes: workspace missing, misaligned or smaller than xd_hist256_workspace_size()");
+    hipStream_t s = (hipStream_t)stream;
+    char *ws = static_cast<char *>(workspace);
+    const uint64_t wbeg = reinterpret_cast<uint64_t>(words), nvec = n / 4;
+    uint64_t pair0 = 0, npairs = 0;  // 16 KiB pairs covering the full vectors
+    if (nvec > 0) {
+        pair0 = (wbeg / kH8Chunk) >> 1;
+        npairs = (((wbeg + 16 * nvec - 1) / kH8Chunk) >> 1) - pair0 + 1;
+    }
+    const uint64_t g8 = (npairs + kNumXcd - 1) / kNumXcd * kNumXcd;
+    const int grid = (int)std::min<uint64_t>(kH8MaxGrid, std::max<uint64_t>(kNumXcd, g8));
+    const HomeMap home{home_attr, wbeg / kHomePage, home_mask()};
+    KernelTimer kt("hist256", s);
+    hipLaunchKernelGGL(hist256_kernel, dim3(grid), dim3(kH8Threads), 0, s, words, (uint64_t)n, pair0, npairs, mode,
+                       home, reinterpret_cast<unsigned long long *>(ws + L.acc),
+                       reinterpret_cast<uint32_t *>(ws + L.sync), counts);
+    return launch_status("hist256_kernel");
+}
+
+}  // extern "C"

@@ -27,6 +27,28 @@ def normal_f16(n: int, mean: float, stddev: float, seed: int) -> np.ndarray:
     return out.view(np.float16)
 
 
+def mix32_words(n: int, seed: int = 0) -> np.ndarray:
+    """The reference histogram's data: words[i] = mix32(i ^ seed) (seed 0 there)."""
+    out = np.empty(n, dtype=np.uint32)
+    _lib.call("xd_gen_mix32_words", out.ctypes.data if n else None, n, seed)
+    return out
+
+
+def mix32_f32(n: int, seed: int, modulus: int = 0, offset: int = 0) -> np.ndarray:
+    """The reference GEMV's init_data values: (h & 0xff)/255 - 0.5, or h % modulus - offset."""
+    out = np.empty(n, dtype=np.float32)
+    _lib.call("xd_gen_mix32_f32", out.ctypes.data if n else None, n, seed, modulus, offset)
+    return out
+
+
+def gemv_mix32_inputs(M: int, K: int, seed: int = SEED_GEMV_F32, integer: bool = False):
+    """A[M,K], x[K] exactly as the reference's init_data draws them (GEMV.cu:118-139)."""
+    if integer:
+        return (mix32_f32(M * K, seed, 17, 8).reshape(M, K),
+                mix32_f32(K, (seed + X_SEED_OFFSET) & 0xFFFFFFFF, 7, 3))
+    return mix32_f32(M * K, seed).reshape(M, K), mix32_f32(K, (seed + X_SEED_OFFSET) & 0xFFFFFFFF)
+
+
 def zipf_thresholds(num_bins: int, s: float = 1.1) -> np.ndarray:
     out = np.empty(num_bins, dtype=np.uint64)
     _lib.call("xd_zipf_thresholds", out.ctypes.data, num_bins, s)

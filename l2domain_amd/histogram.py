@@ -51,3 +51,27 @@ class Histogram:
 
 def histogram(keys: torch.Tensor, num_bins: int, mode="aware") -> torch.Tensor:
     return Histogram(max(keys.numel(), 1), num_bins, keys.device)(keys, mode=mode)
+
+
+class ByteHistogram:
+    """The reference's own histogram: 256 bins, every byte of every uint32 word counted
+    (add_word, histogram256_sideaware.cu:20-25). Owns the workspace of xd_hist256_u32bytes;
+    `home_attr` is the xd_home_map of the words buffer the aware mode routes by."""
+
+    def __init__(self, device: int | str = 0):
+        dev = torch.device(f"cuda:{device}" if isinstance(device, int) else device)
+        nbytes = int(_lib.lib.xd_hist256_workspace_size())
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)  # left zeroed by every call
+
+    def __call__(self, words: torch.Tensor, counts: torch.Tensor | None = None, mode="aware",
+                 home_attr: torch.Tensor | None = None, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+        if words.dtype not in (torch.int32, torch.uint32) or words.dim() != 1:
+            raise TypeError("words must be a 1-D 32-bit integer tensor")
+        n = words.numel()
+        if counts is None:
+            counts = torch.empty(256, dtype=torch.int32, device=words.device)
+        if counts.numel() != 256 or counts.element_size() != 4:
+            raise ValueError("counts must hold 256 32-bit counters")
+        _lib.call("xd_hist256_u32bytes", ptr(words) if n else None, n, ptr(counts), mode_id(mode),
+                  ptr(home_attr), ptr(self.workspace), self.workspace.numel(), stream_handle(stream))
+        return counts

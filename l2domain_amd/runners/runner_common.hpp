@@ -45,14 +45,22 @@ namespace runner {
 // Positional arguments; "--key=value" options are collected separately by Options.
 struct Options {
     std::vector<std::string> pos;
+    std::vector<std::pair<std::string, std::string>> kv;  // other --key=value options
     std::string csv;        // --csv=FILE: append one CSV row (header written if the file is new)
     bool help = false;
     Options(int argc, char **argv) {
         for (int i = 1; i < argc; ++i) {
+            const char *eq = strchr(argv[i], '=');
             if (!strncmp(argv[i], "--csv=", 6)) csv = argv[i] + 6;
             else if (!strcmp(argv[i], "--help") || !strcmp(argv[i], "-h")) help = true;
+            else if (!strncmp(argv[i], "--", 2) && eq) kv.emplace_back(std::string(argv[i] + 2, (size_t)(eq - argv[i] - 2)), std::string(eq + 1));
             else pos.emplace_back(argv[i]);
         }
+    }
+    std::string opt(const char *key, const char *dflt) const {
+        for (auto &p : kv)
+            if (p.first == key) return p.second;
+        return dflt;
     }
     long long geti(size_t i, long long dflt) const { return i < pos.size() ? atoll(pos[i].c_str()) : dflt; }
     double getd(size_t i, double dflt) const { return i < pos.size() ? atof(pos[i].c_str()) : dflt; }

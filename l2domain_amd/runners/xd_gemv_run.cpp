@@ -2,14 +2,18 @@
 // benchmark (applications/gemv/src/gemv_k1024_persistent_subwarp.cu:234-402, parsed by
 // applications/gemv/run.sh:63-97), on libxdom's XCD-oblivious / aware / rotated GEMV.
 //
-//   xd_gemv_run [M=2048] [runs=100] [seed=4242] [flush_l2=0] [K=1024] [dtype=f32|f16] [--csv=FILE]
+//   xd_gemv_run [M=2048] [runs=100] [seed=4242] [flush_l2=0] [K=1024] [dtype=f32|f16]
+//               [init=mix32|mix32int|uniform] [--csv=FILE]
 //
 // M, runs, seed and flush_l2 mean what they mean in the reference (M >= 1024; flush_l2=1
-// evicts every XCD's L2 and the Infinity Cache before each timed repeat). K and dtype are
-// new trailing arguments (the reference fixes K = 1024, fp32). Inputs: fp32 A, x ~ U[-1,1)
-// from xd_gen_uniform_f32(seed) and (seed + 0x9E37); fp16 W ~ N(0, 0.02) from seed, x ~
-// N(0, 1) from seed + 1. "baseline" is XD_MODE_OBLIVIOUS, "aware" XD_MODE_AWARE (memory-home
-// routing with the measured home map of A), "swapped" XD_MODE_ROTATED.
+// evicts every XCD's L2 and the Infinity Cache before each timed repeat). K, dtype and init
+// are new trailing arguments (the reference fixes K = 1024, fp32). fp32 inputs: by default
+// the reference's own init_data (:118-139, xd_gen_mix32_f32): A[i] = (mix32(i ^ seed) &
+// 0xff) / 255 - 0.5 and x[i] the same with seed + 0x9e37; mix32int is its
+// INTEGER_FLOAT_INPUTS variant (exact sums); uniform draws U[-1,1) from xd_gen_uniform_f32.
+// fp16: W ~ N(0, 0.02) from seed, x ~ N(0, 1) from seed + 1. "baseline" is
+// XD_MODE_OBLIVIOUS, "aware" XD_MODE_AWARE (memory-home routing with the measured home map
+// of A), "swapped" XD_MODE_ROTATED.
 //
 // Correctness: the reference's CPU loop (fp32, k ascending, :383-390) and max |y - ref|;
 // exit 3 when an fp32 run exceeds 1e-3 (the pass rule of run.sh:94-97) or an fp16 run
@@ -45,7 +49,8 @@ static float half_to_float(uint16_t h) {
 int main(int argc, char **argv) {
     Options o(argc, argv);
     if (o.help) {
-        printf("usage: %s [M=2048] [runs=100] [seed=4242] [flush_l2=0] [K=1024] [dtype=f32|f16] [--csv=FILE]\n",
+        printf("usage: %s [M=2048] [runs=100] [seed=4242] [flush_l2=0] [K=1024] [dtype=f32|f16] "
+               "[init=mix32|mix32int|uniform] [--csv=FILE]\n",
                argv[0]);
         return 0;
     }
@@ -56,8 +61,10 @@ int main(int argc, char **argv) {
     const int K = (int)o.geti(4, 1024);
     const std::string dtype = o.gets(5, "f32");
     const bool f16 = dtype == "f16";
-    if (K <= 0 || K % (f16 ? 8 : 4) != 0 || (dtype != "f32" && dtype != "f16")) {
-        fprintf(stderr, "bad K or dtype (K %% %d == 0, dtype f32|f16)\n", f16 ? 8 : 4);
+    const std::string init = o.gets(6, "mix32");
+    if (K <= 0 || K % (f16 ? 8 : 4) != 0 || (dtype != "f32" && dtype != "f16") ||
+        (init != "mix32" && init != "mix32int" && init != "uniform")) {
+        fprintf(stderr, "bad K, dtype or init (K %% %d == 0, dtype f32|f16, init mix32|mix32int|uniform)\n", f16 ? 8 : 4);
         return 2;
     }
     const xd_topology_t topo = topology();
@@ -80,8 +87,14 @@ int main(int argc, char **argv) {
     } else {
         hA32.resize(elems);
         hx32.resize(K);
-        RUN_XD(xd_gen_uniform_f32(hA32.data(), elems, seed));
-        RUN_XD(xd_gen_uniform_f32(hx32.data(), K, seed + 0x9E37));
+        if (init == "uniform") {
+            RUN_XD(xd_gen_uniform_f32(hA32.data(), elems, seed));
+            RUN_XD(xd_gen_uniform_f32(hx32.data(), K, seed + 0x9E37));
+        } else {
+            const bool integer = init == "mix32int";
+            RUN_XD(xd_gen_mix32_f32(hA32.data(), elems, (uint32_t)seed, integer ? 17u : 0u, integer ? 8 : 0));
+            RUN_XD(xd_gen_mix32_f32(hx32.data(), K, (uint32_t)seed + 0x9e37u, integer ? 7u : 0u, integer ? 3 : 0));
+        }
         RUN_HIP(hipMemcpy(dA, hA32.data(), elems * 4, hipMemcpyHostToDevice));
         RUN_HIP(hipMemcpy(dx, hx32.data(), (size_t)K * 4, hipMemcpyHostToDevice));
     }
@@ -138,8 +151,8 @@ int main(int argc, char **argv) {
     const bool ic = !flush_l2 && bytes <= 256.0 * 1024 * 1024;
 
     printf("=== GEMV (XCD domains): K=%d %s ===\n", K, f16 ? "fp16 weights, fp32 accumulate" : "fp32");
-    printf("gpu=%s M=%d K=%d dtype=%s flush_l2=%d xcds=%d cus=%d workspace=%zu\n", topo.name, M, K, dtype.c_str(),
-           flush_l2, topo.num_xcd, topo.num_cu, wsb);
+    printf("gpu=%s M=%d K=%d dtype=%s init=%s flush_l2=%d xcds=%d cus=%d workspace=%zu\n", topo.name, M, K,
+           dtype.c_str(), f16 ? "normal" : init.c_str(), flush_l2, topo.num_xcd, topo.num_cu, wsb);
     printf("baseline_ms %.6f ms %.2f GFLOP/s\n", ms[0], flops / (ms[0] * 1e6));
     printf("aware_ms %.6f ms aware_speedup=%.3fx %.2f GFLOP/s\n", ms[1], ms[0] / ms[1], flops / (ms[1] * 1e6));
     printf("swapped_ms %.6f ms swapped_speedup=%.3fx %.2f GFLOP/s\n", ms[2], ms[0] / ms[2], flops / (ms[2] * 1e6));
@@ -151,14 +164,17 @@ int main(int argc, char **argv) {
 
     bool pass = true;
     for (double e : err) pass = pass && (f16 ? e <= 2e-2 * refmax : e <= 1e-3);
-    char row[512];
-    snprintf(row, sizeof row, "%d,%d,%s,%.6f,%.6f,%.6f,%.9g,%.6f,%.6f,%.1f,%.4f,%s,%.3f,%s", M, K, dtype.c_str(), ms[0],
+    // the reference's CSV columns (applications/gemv/run.sh:63; lanes per row = one wave64,
+    // waves per workgroup = 4; cublas_ms / aware_vs_cublas come from xd_gemv_vendor_run and
+    // stay empty here), then this build's columns
+    char row[640];
+    snprintf(row, sizeof row, "%d,%d,64,4,%.6f,%.6f,%.6f,,%.9g,%.9f,%.9f,,%s,%s,%s,%.1f,%.4f,%s,%.3f", M, K, ms[0],
              ms[1], ms[2], std::max(err[0], std::max(err[1], err[2])), ms[0] / ms[1], ms[0] / ms[2],
-             bytes / (ms[1] * 1e6), bytes / (ms[1] * 1e6) / 8000.0, ic ? "infinity_cache" : "hbm", cpu_ms,
-             pass ? "PASS" : "FAIL");
+             pass ? "PASS" : "FAIL", dtype.c_str(), f16 ? "normal" : init.c_str(), bytes / (ms[1] * 1e6),
+             bytes / (ms[1] * 1e6) / 8000.0, ic ? "infinity_cache" : "hbm", cpu_ms);
     csv_append(o.csv,
-               "M,K,dtype,baseline_ms,aware_ms,swapped_ms,max_abs_error,aware_speedup,swapped_speedup,aware_gbps,"
-               "roofline_frac,roofline,cpu_ms,pass",
+               "M,K,lanes_per_row,warps_per_block,baseline_ms,aware_ms,swapped_ms,cublas_ms,max_abs_error,"
+               "aware_speedup,swapped_speedup,aware_vs_cublas,pass,dtype,init,aware_gbps,roofline_frac,roofline,cpu_ms",
                row);
     for (auto p : dy) (void)hipFree(p);
     (void)hipFree(dA);

@@ -34,13 +34,7 @@ static int insert_lookup(const Options &o);
 
 int main(int argc, char **argv) {
     Options o(argc, argv);
-    std::string workload = "dep";
-    std::vector<std::string> pos;
-    for (auto &a : o.pos) {
-        if (!a.compare(0, 11, "--workload=")) workload = a.substr(11);
-        else pos.push_back(a);
-    }
-    o.pos = pos;
+    const std::string workload = o.opt("workload", "dep");
     if (o.help || (o.pos.size() != 0 && o.pos.size() != 7) || (workload != "dep" && workload != "insert_lookup")) {
         fprintf(stderr, "Usage: %s [--workload=dep|insert_lookup] K Q C L h H runs [--csv=FILE]\n", argv[0]);
         return o.help ? 0 : 2;

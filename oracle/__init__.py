@@ -40,6 +40,9 @@ _SIGS = {
     "ora_zipf_key_at": (U32, [VP, U32, U64, I, U64]),
     "ora_zipf_scramble": (U32, [U32, U32]),
     "ora_histogram": (U64, [VP, SZ, VP, U32, I]),
+    "ora_gen_mix32_words": (None, [VP, SZ, U32]),
+    "ora_hist256_bytes": (None, [VP, SZ, VP, I]),
+    "ora_gen_mix32_f32": (None, [VP, SZ, U32, U32, C.c_int32]),
     "ora_mix64": (U64, [U64]),
     "ora_hash_kv": (None, [VP, VP, U64, U64]),
     "ora_hash_queries": (None, [VP, U64, U64, U64, U64]),
@@ -140,6 +143,28 @@ def histogram(keys: np.ndarray, num_bins: int, nthreads: int = 1) -> tuple[np.nd
     counts = np.empty(num_bins, dtype=np.uint32)
     c = lib.ora_histogram(_p(keys), keys.size, _p(counts), num_bins, nthreads)
     return counts, int(c)
+
+
+def mix32_words(n: int, seed: int = 0) -> np.ndarray:
+    """HIST.cu:331-340: words[i] = mix32(i ^ seed) (the reference uses seed 0)."""
+    out = np.empty(n, dtype=np.uint32)
+    lib.ora_gen_mix32_words(_p(out), n, seed)
+    return out
+
+
+def hist256_bytes(words: np.ndarray, nthreads: int = 1) -> np.ndarray:
+    """HIST.cu:279-288: every byte of every word counted into 256 bins."""
+    words = np.ascontiguousarray(words).view(np.uint32)
+    counts = np.empty(256, dtype=np.uint32)
+    lib.ora_hist256_bytes(_p(words), words.size, _p(counts), nthreads)
+    return counts
+
+
+def mix32_f32(n: int, seed: int, modulus: int = 0, offset: int = 0) -> np.ndarray:
+    """GEMV.cu:118-139 init_data values (modulus 0: (h & 0xff) / 255 - 0.5)."""
+    out = np.empty(n, dtype=np.float32)
+    lib.ora_gen_mix32_f32(_p(out), n, seed, modulus, offset)
+    return out
 
 
 EMPTY = 0xFFFFFFFFFFFFFFFF

@@ -294,6 +294,58 @@ uint64_t ora_histogram(const uint32_t *keys, size_t n, uint32_t *counts, uint32_
     return total;
 }
 
+/* The reference's own histogram data and loop (HIST.cu:331-340, 279-288): words[i] =
+ * mix32((uint32_t)i ^ seed) (seed 0 in the reference), and every byte of every word
+ * counted into 256 bins. */
+void ora_gen_mix32_words(uint32_t *out, size_t n, uint32_t seed) {
+    for (size_t i = 0; i < n; ++i) out[i] = ora_mix32((uint32_t)i ^ seed);
+}
+
+typedef struct {
+    const uint32_t *w;
+    uint32_t (*priv)[256];
+    int64_t per;
+} h256_ctx;
+
+static void h256_part(void *p, int64_t b, int64_t e) {
+    h256_ctx *c = (h256_ctx *)p;
+    uint32_t *h = c->priv[b / c->per];
+    for (int64_t i = b; i < e; ++i) {
+        const uint32_t w = c->w[i];
+        h[w & 0xffu]++;
+        h[(w >> 8) & 0xffu]++;
+        h[(w >> 16) & 0xffu]++;
+        h[w >> 24]++;
+    }
+}
+
+void ora_hist256_bytes(const uint32_t *words, size_t n, uint32_t *counts, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 256) nthreads = 256;
+    uint32_t(*priv)[256] = (uint32_t(*)[256])calloc((size_t)nthreads, sizeof(*priv));
+    h256_ctx c = {words, priv, (int64_t)((n + nthreads - 1) / nthreads)};
+    if (c.per < 1) c.per = 1;
+    parallel_range((int64_t)n, nthreads, h256_part, &c);
+    memset(counts, 0, 256 * sizeof(uint32_t));
+    for (int t = 0; t < nthreads; ++t)
+        for (int k = 0; k < 256; ++k) counts[k] += priv[t][k];
+    free(priv);
+}
+
+/* GEMV init_data (GEMV.cu:118-139): h = mix32((uint32_t)i ^ seed); the default inputs are
+ * (float)(h & 0xff) / 255.0f - 0.5f, the INTEGER_FLOAT_INPUTS ones (int)(h % modulus) - offset. */
+void ora_gen_mix32_f32(float *out, size_t n, uint32_t seed, uint32_t modulus, int32_t offset) {
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t h = ora_mix32((uint32_t)i ^ seed);
+        if (modulus) {
+            out[i] = (float)((int32_t)(h % modulus) - offset);
+        } else {
+            const float q = (float)(h & 0xffu) / 255.0f;
+            out[i] = q - 0.5f;
+        }
+    }
+}
+
 /* ------------------------------------------------------------------------------------ */
 /* hash table                                                                            */
 /* ------------------------------------------------------------------------------------ */

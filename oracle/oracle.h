@@ -42,6 +42,13 @@ uint32_t ora_zipf_key_at(const uint64_t *t, uint32_t num_bins, uint64_t seed, in
 /* counts[k] = #{i : keys[i] == k}; keys >= num_bins are not counted. Returns the number counted. */
 uint64_t ora_histogram(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int nthreads);
 
+/* The reference's own histogram (HIST.cu:279-288, 331-340): words[i] = mix32(i ^ seed), every
+ * byte of every word counted into 256 bins (nthreads private histograms, summed). */
+void ora_gen_mix32_words(uint32_t *out, size_t n, uint32_t seed);
+void ora_hist256_bytes(const uint32_t *words, size_t n, uint32_t *counts, int nthreads);
+/* GEMV init_data (GEMV.cu:118-139): (h & 0xff) / 255 - 0.5 (modulus 0) or h % modulus - offset. */
+void ora_gen_mix32_f32(float *out, size_t n, uint32_t seed, uint32_t modulus, int32_t offset);
+
 /* ---- hash table (HASH.cu:46-64 probe, HASH.cu:226-241 serial CPU insert; u64 keys+values) ---- */
 uint64_t ora_mix64(uint64_t z); /* splitmix64 output function */
 void ora_hash_kv(uint64_t *keys, uint64_t *vals, uint64_t n, uint64_t seed);

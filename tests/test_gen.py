@@ -31,3 +31,14 @@ def test_gemv_inputs_shapes_and_seeds():
     np.testing.assert_array_equal(x, ora.uniform_f32(16, 4242 + 0x9E37))
     W, xh = gen.gemv_f16_inputs(4, 8)
     assert W.dtype == np.float16 and xh.dtype == np.float16
+
+
+def test_mix32_generators_match_oracle():
+    n = (1 << 17) + 5
+    for seed in (0, 4242, 0xFFFFFFFF):
+        np.testing.assert_array_equal(gen.mix32_words(n, seed), ora.mix32_words(n, seed))
+        for mod, off in ((0, 0), (17, 8), (7, 3)):
+            np.testing.assert_array_equal(gen.mix32_f32(n, seed, mod, off).view(np.uint32),
+                                          ora.mix32_f32(n, seed, mod, off).view(np.uint32))
+    A, x = gen.gemv_mix32_inputs(4, 1024)
+    np.testing.assert_array_equal(x, ora.mix32_f32(1024, 4242 + 0x9E37))

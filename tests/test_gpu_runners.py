@@ -41,11 +41,33 @@ def test_gemv_runner(tmp_path, K, dtype):
     if dtype == "f32":
         assert max(errs) <= 1e-3  # applications/gemv/run.sh:94-97
     rows = (tmp_path / "g.csv").read_text().splitlines()
-    assert rows[0].startswith("M,K,dtype,baseline_ms") and rows[1].endswith(",PASS")
+    assert rows[0].startswith("M,K,lanes_per_row,warps_per_block,baseline_ms,aware_ms,swapped_ms,cublas_ms")
+    assert rows[1].split(",")[12] == "PASS"
 
 
-def test_hist_runner(tmp_path):
-    rc, out, err = run("xd_hist_run", 16, 2, 256, 1, 0, 1 << 20, 1.1, 1373, csv=tmp_path / "h.csv")
+@pytest.mark.parametrize("init", ["mix32", "mix32int"])
+def test_gemv_runner_reference_inputs(init):
+    """The reference's own inputs (init_data) at its K = 1024 with M = 2048 (the quick preset)."""
+    rc, out, err = run("xd_gemv_run", 2048, 5, 4242, 1, 1024, "f32", init)
+    assert rc == 0, out + err
+    line = next(l for l in out.splitlines() if l.startswith("correctness max_abs_error"))
+    errs = [float(t.split("=")[1]) for t in line.split() if "=" in t]
+    assert max(errs) <= 1e-3
+    if init == "mix32int":
+        assert max(errs) == 0.0  # integer-valued inputs: every summation order is exact
+
+
+def test_gemv_vendor_runner():
+    rc, out, err = run("xd_gemv_vendor_run", 2048, 1024, 5, 1, 1)
+    assert rc == 0, out + err
+    assert float(first_field(out, "cublas_ms")) > 0 and "vendor=rocblas" in out
+
+
+@pytest.mark.parametrize("args", [("--workload=zipf", 16, 2, 256, 1, 0, 1 << 20, 1.1, 1373), (32, 2, 128, 1, 0)])
+def test_hist_runner(tmp_path, args):
+    """(32, 2, 128, 1, 0): the reference's quick preset (data_mb 32, THREADS=128, BLOCKS_PER_SM=1,
+    CACHE_MODE=0) on its own byte-histogram workload."""
+    rc, out, err = run("xd_hist_run", *args, csv=tmp_path / "h.csv")
     assert rc == 0, out + err
     line = next(l for l in out.splitlines() if l.startswith("correct "))
     assert line.split()[1:] == ["baseline=PASS", "green_aware=PASS", "green_swapped=PASS", "persistent_aware=PASS",

@@ -372,3 +372,43 @@ def test_dep_make_keys_pools_and_queries():
     hot0, hot1 = set(keys[:H].tolist()), set(keys[H:2 * H].tolist())
     assert all((x in hot1) if i % 2 else (x in hot0) for i, x in enumerate(q[:800].tolist()))
     assert set(q.tolist()) <= set(keys.tolist())
+
+
+def test_hist256_oracle_matches_numpy_byte_bincount():
+    """HIST.cu:279-288: the byte histogram equals numpy's bincount of the words' bytes (an
+    independent method), sums to 4 n, and does not depend on the thread split."""
+    rng = np.random.default_rng(5)
+    for n in (0, 1, 7, 4096, 100003):
+        w = rng.integers(0, 1 << 32, size=n, dtype=np.uint64).astype(np.uint32)
+        ref = np.bincount(w.view(np.uint8), minlength=256).astype(np.uint32)
+        got = ora.hist256_bytes(w)
+        np.testing.assert_array_equal(got, ref)
+        assert int(got.sum()) == 4 * n
+        np.testing.assert_array_equal(ora.hist256_bytes(w, nthreads=7), ref)
+    w = np.full(1000, 0x01010203, dtype=np.uint32)
+    got = ora.hist256_bytes(w)
+    assert got[1] == 2000 and got[2] == 1000 and got[3] == 1000 and got.sum() == 4000
+
+
+def test_mix32_words_are_the_reference_data():
+    """HIST.cu:331-340 words[i] = mix32(i): first values are the lowbias32 known answers."""
+    w = ora.mix32_words(5)
+    assert [int(v) for v in w[:3]] == [0, 0x688990C0, 0xD1132181]
+    assert int(ora.mix32_words(1, seed=4242)[0]) == 0xE0D78B3B  # mix32(0 ^ 4242)
+
+
+def test_gemv_mix32_init_known_answers():
+    """GEMV.cu:118-139 init_data at index 0 with the reference's seed 4242: h = mix32(4242)
+    = 0xe0d78b3b, so A[0] = float(0x3b) / 255 - 0.5 (binary32 ops) and, in the integer
+    variant, A[0] = 0xe0d78b3b % 17 - 8."""
+    a = ora.mix32_f32(3, 4242)
+    assert a[0] == np.float32(np.float32(0x3B) / np.float32(255.0)) - np.float32(0.5)
+    ai = ora.mix32_f32(3, 4242, 17, 8)
+    assert ai[0] == float(0xE0D78B3B % 17 - 8)
+    h = ora.mix32(1 ^ 4242)
+    assert ai[1] == float(h % 17 - 8) and a[1] == np.float32(np.float32(h & 0xFF) / np.float32(255.0)) - np.float32(0.5)
+    vals = ora.mix32_f32(1 << 16, 7)
+    grid = np.float32(np.arange(256, dtype=np.float32) / np.float32(255.0)) - np.float32(0.5)
+    assert np.isin(vals, grid).all()
+    xi = ora.mix32_f32(1 << 12, 7 + 0x9E37, 7, 3)
+    assert xi.min() == -3 and xi.max() == 3

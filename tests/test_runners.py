@@ -6,7 +6,7 @@ from pathlib import Path
 import pytest
 
 BIN = Path(__file__).resolve().parents[1] / "l2domain_amd" / "bin"
-RUNNERS = ["xd_gemv_run", "xd_hist_run", "xd_hash_run", "xd_bfs_run", "xd_arch_probe"]
+RUNNERS = ["xd_gemv_run", "xd_gemv_vendor_run", "xd_hist_run", "xd_hash_run", "xd_bfs_run", "xd_arch_probe"]
 
 
 @pytest.mark.parametrize("name", RUNNERS)
@@ -28,6 +28,10 @@ def test_runner_argument_checks():
     r = subprocess.run([str(BIN / "xd_gemv_run"), "1024", "1", "1", "0", "6", "f32"], capture_output=True, text=True,
                        timeout=60)
     assert r.returncode == 2
-    r = subprocess.run([str(BIN / "xd_hist_run"), "1", "1", "256", "1", "1", str(1 << 25)], capture_output=True,
-                       text=True, timeout=60)
+    r = subprocess.run([str(BIN / "xd_hist_run"), "--workload=zipf", "1", "1", "256", "1", "1", str(1 << 25)],
+                       capture_output=True, text=True, timeout=60)
     assert r.returncode == 2
+    r = subprocess.run([str(BIN / "xd_hist_run"), "--workload=other"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2
+    r = subprocess.run([str(BIN / "xd_hist_run"), "4096"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2  # 4096 MiB of words would overflow the u32 byte counts

@@ -9,7 +9,7 @@ steps timed with HIP events on the stream the kernels are launched on. Prints ON
 `value` is the XCD-aware variant's throughput; the oblivious and rotated variants are
 timed over the same K steps and reported beside it with the aware/oblivious speedup.
 Unless --only is given, every other configuration (GEMV fp32 and fp16 warm and cold, hash,
-the reference's dependent probe and byte histogram, BFS) is measured the same way, with at most 50 timed steps, under "extras".
+the reference's dependent probe, byte histogram and fixed-depth BFS, BFS) is measured the same way, with at most 50 timed steps, under "extras".
 """
 from __future__ import annotations
 
@@ -374,6 +374,70 @@ class Hist256:
                           f"{nt} threads with private histograms)"}
 
 
+class BfsRef:
+    """The reference's own BFS workload at its paper preset (applications/bfs/run.sh:24-27):
+    2,000,000 vertices of degree 64 in its directed hot-pool graph (hot_per_side 200,000,
+    dst_local 95 %, seed 8201; sides from the measured homes of this run's buffers), 4096
+    sources, 4 top-down levels. A step = one whole search, initialisation included."""
+    name = "bfs_ref_V2M_deg64_src4096_depth4"
+    unit = "GTEPS"
+    dtype = "int32"
+    dominant = "bfs_multi"
+
+    def __init__(self):
+        import numpy as np
+        from l2domain_amd.bfs import REF_PAPER, RefGraph, ref_clamp
+        p = REF_PAPER
+        self.V, self.deg, self.nsrc, self.depth, self.dl, self.H = ref_clamp(
+            p["vertices"], p["degree"], p["sources"], p["depth"], p["dst_local_pct"], p["hot_per_side"])
+        self.g = RefGraph(self.V, self.deg, self.nsrc, self.dl, self.H, p["seed"])
+        import oracle as ora
+        self.ref, self.reached = ora.bfs_multi(self.g.h_rowptr, self.g.h_col, self.g.h_sources, self.depth)
+        expanded = (self.ref != 0xFFFFFFFF) & (self.ref < self.depth)
+        self.edges = int(np.diff(self.g.h_rowptr.astype(np.int64))[expanded].sum())
+        self.nexp = int(expanded.sum())
+        self.np = np
+
+    def step(self, mode):
+        self.g.bfs(self.depth, mode=mode)
+
+    def throughput(self, sec_per_step):
+        return self.edges / sec_per_step / 1e9
+
+    def verify(self):
+        ok = True
+        for mode in MODES:
+            self.step(mode)
+            got = self.g.level.cpu().numpy().view(self.np.uint32)
+            ok = ok and bool(self.np.array_equal(got, self.ref))
+        return ok
+
+    def roofline(self, sec_per_launch):
+        # adjacency lists of the expanded vertices, their two rowptr entries, and the level
+        # array written once (initialisation)
+        nbytes = 4 * self.edges + 8 * self.nexp + 4 * self.V
+        achieved = nbytes / sec_per_launch / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "bfs search (multi_init/seed/level kernels)", "algorithmic_bytes_per_bfs": nbytes}
+
+    def config(self):
+        return {"workload": self.name, "vertices": self.V, "degree": self.deg, "sources": self.nsrc,
+                "depth": self.depth, "dst_local_pct": self.dl, "hot_per_side": self.H, "seed": 8201,
+                "edges_walked": self.edges, "reached": self.reached}
+
+    def cpu_baseline(self):
+        import oracle as ora
+        t0 = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t0 < 5.0:
+            ora.bfs_multi(self.g.h_rowptr, self.g.h_col, self.g.h_sources, self.depth)
+            reps += 1
+        dt = (time.perf_counter() - t0) / reps
+        return {"value": round(self.edges / dt / 1e9, 4), "unit": "GTEPS", "cores": 1, "kind": "port",
+                "sample": f"{reps} full serial multi-source searches of the same graph (oracle, bfs.cu:215-252)"}
+
+
 class HashDep:
     """The reference's own hash workload (hash_probe_dep.cu, defaults :124-130): K = 32000000
     int32 keys with successors in 2^26 8-byte entries, two hot pools of 100000 keys homed on
@@ -505,6 +569,7 @@ WORKLOADS = {
     "hash": Hash,
     "hash_dep": HashDep,
     "hist256": Hist256,
+    "bfs_ref": BfsRef,
     "gemv_f32": GemvF32,
     "gemv_f16_up": lambda: GemvF16(14336, 4096),
     "gemv_f16_down": lambda: GemvF16(4096, 14336),
@@ -513,7 +578,7 @@ DEFAULT_WORKLOAD = "hist"
 # every other BASELINE config, reported under "extras" of the same JSON line
 EXTRAS = (("gemv_f32", False), ("gemv_f32", True), ("gemv_f16_up", False), ("gemv_f16_up", True),
           ("gemv_f16_down", False), ("gemv_f16_down", True), ("hash", False), ("hash_dep", False),
-          ("bfs", False), ("hist256", True), ("hist256", False))
+          ("bfs", False), ("hist256", True), ("hist256", False), ("bfs_ref", False))
 
 
 # ---------------------------------------------------------------------------------------

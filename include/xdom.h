@@ -332,6 +332,36 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t num_vertices, 
                uint32_t *level, int mode, const void *route, void *workspace, size_t workspace_bytes,
                void *stream, xd_bfs_stats_t *stats);
 
+/* The reference's own BFS workload. */
+
+/* Host generator of the reference's directed fixed-degree graph (bfs.cu:354-409): rowptr[V+1],
+ * col[V * degree], work_side[V] (the die that works on each vertex) and sources[num_sources].
+ * The sides come from the homes of the device buffers the graph will live in: col_addr /
+ * level_addr are the device addresses of col and of the level array, *_home_host host copies
+ * of their xd_home_map (NULL: the address-mask prediction). Neighbour j of v is drawn as
+ * xd_rand64(seed, v * degree + j) mod hot_per_side (the reference uses std::mt19937). Returns
+ * XD_ERR_UNSUPPORTED when either hot pool cannot be filled (the reference exits with 2). */
+int xd_bfs_ref_graph(int32_t num_vertices, int32_t degree, int32_t num_sources, int32_t dst_local_pct,
+                     int32_t hot_per_side, uint64_t seed, uint64_t col_addr, const uint8_t *col_home_host,
+                     uint64_t level_addr, const uint8_t *level_home_host, int32_t *rowptr, int32_t *col,
+                     uint8_t *work_side, int32_t *sources);
+
+/* Workspace bytes of xd_bfs_multi (about 24 bytes per vertex). No zeroing needed. */
+size_t xd_bfs_multi_workspace_size(int32_t num_vertices);
+
+/* Multi-source, fixed-depth top-down BFS over a directed CSR graph: level[v] = the distance
+ * from the nearest source when at most max_depth, XD_BFS_UNVISITED otherwise. Sources and col
+ * entries must lie in [0, V). The whole search is enqueued on `stream` (no host round trip).
+ * Replaces init_dist_kernel / seed_*_kernel / luo_baseline_level_kernel /
+ * luo_side_level_kernel and the fixed-depth host loops (applications/bfs/src/bfs.cu:151-308,
+ * 449-491). Modes: XD_MODE_OBLIVIOUS, one frontier consumed by every workgroup; XD_MODE_AWARE,
+ * one frontier per I/O die, die d consuming the vertices with work_side == d and winners
+ * going to the frontier of their work side (the reference's aware run); XD_MODE_ROTATED, die
+ * d consuming the other die's frontier (swapped). */
+int xd_bfs_multi(const int32_t *rowptr, const int32_t *col, int32_t num_vertices, int64_t nnz,
+                 const int32_t *sources, int32_t num_sources, int32_t max_depth, const uint8_t *work_side,
+                 uint32_t *level, int mode, void *workspace, size_t workspace_bytes, void *stream);
+
 /* ------------------------------------------------------------------------------------ */
 /* Seeded input generators (host). Fully specified integer mixers; no libc RNG.          */
 /* ------------------------------------------------------------------------------------ */

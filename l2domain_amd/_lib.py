@@ -103,6 +103,10 @@ SIGNATURES: dict[str, tuple] = {
     "xd_bfs_route_bytes": (SZ, [C.c_int32]),
     "xd_bfs_route": (I, [VP, VP, C.c_int32, I64, VP, VP, SZ, VP]),
     "xd_bfs_csr": (I, [VP, VP, C.c_int32, I64, C.c_int32, VP, I, VP, VP, SZ, VP, C.POINTER(BfsStats)]),
+    "xd_bfs_ref_graph": (I, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, U64, U64, VP, U64, VP, VP, VP, VP,
+                             VP]),
+    "xd_bfs_multi_workspace_size": (SZ, [C.c_int32]),
+    "xd_bfs_multi": (I, [VP, VP, C.c_int32, I64, VP, C.c_int32, C.c_int32, VP, VP, I, VP, SZ, VP]),
     "xd_rand64": (U64, [U64, U64]),
     "xd_gen_uniform_f32": (I, [VP, SZ, U64]),
     "xd_gen_normal_f16": (I, [VP, SZ, D, D, U64]),

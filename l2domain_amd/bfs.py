@@ -1,4 +1,5 @@
-"""Direction-optimizing BFS over an undirected CSR graph, and the R-MAT generator.
+"""Direction-optimizing BFS over an undirected CSR graph, the R-MAT generator, and the
+reference's own multi-source fixed-depth workload over its hot-pool graph.
 
 Mirrors the reference BFS application (applications/bfs/src/bfs.cu): "baseline"/"oblivious"
 is the all-SM launch (luo_baseline_level_kernel, :215-252), "aware" the per-side launch
@@ -63,3 +64,73 @@ class Graph:
         return self.level, {"levels": st.levels, "topdown_steps": st.topdown_steps,
                             "bottomup_steps": st.bottomup_steps, "reached_vertices": st.reached_vertices,
                             "reached_edges": st.reached_edges}
+
+
+# The reference's own BFS workload (applications/bfs/run.sh presets; bfs.cu defaults :329-336)
+REF_PAPER = dict(vertices=2000000, degree=64, sources=4096, depth=4, dst_local_pct=95, hot_per_side=200000,
+                 seed=8201)
+REF_QUICK = dict(vertices=65536, degree=8, sources=128, depth=2, dst_local_pct=95, hot_per_side=4096, seed=8201)
+
+
+def ref_clamp(vertices, degree, sources, depth, dst_local_pct, hot_per_side):
+    """The reference's argument clamps (bfs.cu:338-343)."""
+    vertices = max(vertices, 4096)
+    degree = max(degree, 1)
+    sources = max(1, min(sources, vertices // 4))
+    depth = max(1, depth)
+    dst_local_pct = max(0, min(dst_local_pct, 100))
+    hot_per_side = max(1024, min(hot_per_side, vertices // 3))
+    return vertices, degree, sources, depth, dst_local_pct, hot_per_side
+
+
+class RefGraph:
+    """The reference's directed hot-pool graph (xd_bfs_ref_graph), resident on the device with
+    the buffers it was generated for: the sides of its vertices come from the measured homes
+    of its own col and level arrays, as the reference derives them from its buffers."""
+
+    def __init__(self, vertices: int, degree: int, sources: int, dst_local_pct: int, hot_per_side: int,
+                 seed: int = 8201, device: int | str = 0, map_homes: bool = True):
+        from .domain import home_map
+        dev = torch.device(f"cuda:{device}" if isinstance(device, int) else device)
+        V = self.V = int(vertices)
+        self.degree, self.nsrc = int(degree), int(sources)
+        self.nnz = V * self.degree
+        self.col = torch.empty(max(self.nnz, 1), dtype=torch.int32, device=dev)
+        self.level = torch.empty(V, dtype=torch.int32, device=dev)
+        ch = home_map(self.col).cpu().numpy() if map_homes else None
+        lh = home_map(self.level).cpu().numpy() if map_homes else None
+        self.col_home, self.level_home = ch, lh
+        self.h_rowptr = np.empty(V + 1, dtype=np.int32)
+        self.h_col = np.empty(self.nnz, dtype=np.int32)
+        self.h_work_side = np.empty(V, dtype=np.uint8)
+        self.h_sources = np.empty(max(self.nsrc, 1), dtype=np.int32)
+        _lib.call("xd_bfs_ref_graph", V, self.degree, self.nsrc, dst_local_pct, hot_per_side, seed, ptr(self.col),
+                  None if ch is None else ch.ctypes.data, ptr(self.level), None if lh is None else lh.ctypes.data,
+                  self.h_rowptr.ctypes.data, self.h_col.ctypes.data, self.h_work_side.ctypes.data,
+                  self.h_sources.ctypes.data)
+        self.h_sources = self.h_sources[: self.nsrc]
+        self.col[: self.nnz].copy_(torch.from_numpy(self.h_col))
+        self.rowptr = torch.from_numpy(self.h_rowptr).to(dev)
+        self.work_side = torch.from_numpy(self.h_work_side).to(dev)
+        self.sources = torch.from_numpy(self.h_sources).to(dev)
+        ws = int(_lib.lib.xd_bfs_multi_workspace_size(V))
+        self.workspace = torch.empty(ws, dtype=torch.uint8, device=dev)
+
+    def bfs(self, max_depth: int, mode="aware", level: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        out = self.level if level is None else level
+        _lib.call("xd_bfs_multi", ptr(self.rowptr), ptr(self.col), self.V, self.nnz, ptr(self.sources), self.nsrc,
+                  max_depth, ptr(self.work_side), ptr(out), mode_id(mode), ptr(self.workspace),
+                  self.workspace.numel(), stream_handle(stream))
+        return out
+
+
+def bfs_multi(rowptr: torch.Tensor, col: torch.Tensor, sources: torch.Tensor, max_depth: int, mode="oblivious",
+              work_side: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Multi-source fixed-depth BFS over any directed device CSR (xd_bfs_multi)."""
+    V = rowptr.numel() - 1
+    ws = torch.empty(int(_lib.lib.xd_bfs_multi_workspace_size(V)), dtype=torch.uint8, device=rowptr.device)
+    level = torch.empty(V, dtype=torch.int32, device=rowptr.device)
+    _lib.call("xd_bfs_multi", ptr(rowptr), ptr(col) if col.numel() else None, V, col.numel(),
+              ptr(sources) if sources.numel() else None, sources.numel(), max_depth, ptr(work_side), ptr(level),
+              mode_id(mode), ptr(ws), ws.numel(), stream_handle(stream))
+    return level

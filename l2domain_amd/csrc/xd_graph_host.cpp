@@ -1,4 +1,5 @@
-// R-MAT graph generator producing an undirected CSR graph (host, multi-threaded).
+// Graph generators (host, multi-threaded): the build's undirected R-MAT graph and the
+// reference's own directed hot-pool graph.
 //
 // The reference's BFS input is a synthetic fixed-degree graph drawn from two "hot pools"
 // with std::mt19937 (applications/bfs/src/bfs.cu:354-409). The BFS configuration of this
@@ -122,6 +123,60 @@ int xd_rmat_csr(int scale, int edge_factor, double a, double b, double c, uint64
         for (size_t v = lo; v < hi; ++v) memcpy(col + rowptr[v], tmp.data() + off[v], sizeof(int32_t) * (size_t)ndeg[v]);
     });
     *nnz_out = rowptr[V];
+    return XD_OK;
+}
+
+
+// The reference's BFS graph (applications/bfs/src/bfs.cu:354-409). A vertex's side is the
+// die homing the start of its adjacency row (col + v * degree); its level entry's die must
+// agree for it to enter the hot pool of that side (the first hot_per_side such vertices per
+// side, in vertex order). The last cross_per_side = hot_per_side * (100 - dst_local_pct) /
+// 100 hot vertices of each pool draw their neighbours from the other pool and are worked on
+// by the other side; every other vertex draws from its own side's pool. Neighbour j of v is
+// pool[xd_rand64(seed, v * degree + j) mod hot_per_side] (the reference draws from
+// std::mt19937(seed)); source i is hot1[(i / 2) mod H] for odd i, hot0[(i / 2) mod H] for even.
+int xd_bfs_ref_graph(int32_t V, int32_t degree, int32_t num_sources, int32_t dst_local_pct, int32_t hot_per_side,
+                     uint64_t seed, uint64_t col_addr, const uint8_t *col_home_host, uint64_t level_addr,
+                     const uint8_t *level_home_host, int32_t *rowptr, int32_t *col, uint8_t *work_side,
+                     int32_t *sources) {
+    if (V < 1 || degree < 1 || (int64_t)V * degree >= (1ll << 31) || num_sources < 0 || dst_local_pct < 0 ||
+        dst_local_pct > 100 || hot_per_side < 1 || !rowptr || !col || !work_side || (num_sources > 0 && !sources))
+        return XD_ERR_INVALID_ARG;
+    const uint64_t mask = xd_home_mask();
+    auto side = [&](uint64_t addr, uint64_t base, const uint8_t *attr) -> uint8_t {
+        if (attr) return (uint8_t)(((addr >> 13) & 1u) ^ attr[(addr >> 21) - (base >> 21)]);
+        return (uint8_t)(__builtin_popcountll(addr & mask) & 1);
+    };
+    std::vector<int32_t> hot[2];
+    hot[0].reserve((size_t)hot_per_side);
+    hot[1].reserve((size_t)hot_per_side);
+    for (int32_t v = 0; v < V; ++v) {
+        const uint8_t rs = side(col_addr + (uint64_t)v * (uint64_t)degree * 4u, col_addr, col_home_host);
+        const uint8_t ds = side(level_addr + (uint64_t)v * 4u, level_addr, level_home_host);
+        work_side[v] = rs;
+        if (rs == ds && (int32_t)hot[rs].size() < hot_per_side) hot[rs].push_back(v);
+    }
+    if ((int32_t)hot[0].size() < hot_per_side || (int32_t)hot[1].size() < hot_per_side) return XD_ERR_UNSUPPORTED;
+    std::vector<uint8_t> dst_side(work_side, work_side + V);
+    const int32_t cross = (int32_t)((int64_t)hot_per_side * (100 - dst_local_pct) / 100);
+    for (int32_t i = 0; i < cross; ++i) {
+        const int32_t v0 = hot[0][(size_t)(hot_per_side - 1 - i)], v1 = hot[1][(size_t)(hot_per_side - 1 - i)];
+        dst_side[v0] = 1;  // its neighbours come from the other pool ...
+        dst_side[v1] = 0;
+        work_side[v0] = 1;  // ... and the other side works on it
+        work_side[v1] = 0;
+    }
+    const uint64_t H = (uint64_t)hot_per_side;
+    par((size_t)V, [&](size_t b, size_t e) {
+        for (size_t v = b; v < e; ++v) {
+            rowptr[v] = (int32_t)(v * (size_t)degree);
+            const std::vector<int32_t> &pool = hot[dst_side[v]];
+            for (int32_t j = 0; j < degree; ++j)
+                col[v * (size_t)degree + (size_t)j] = pool[(size_t)(rnd(seed, (uint64_t)v * (uint64_t)degree + (uint64_t)j) % H)];
+        }
+    });
+    rowptr[V] = (int32_t)((int64_t)V * degree);
+    for (int32_t i = 0; i < num_sources; ++i) sources[i] = hot[i & 1][(size_t)((i / 2) % hot_per_side)];
     return XD_OK;
 }
 

@@ -51,6 +51,9 @@ _SIGS = {
     "ora_rmat_edge": (None, [I, D, D, D, U64, U64, C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     "ora_rmat_csr": (I64, [I, I, D, D, D, U64, VP, VP]),
     "ora_bfs": (I64, [VP, VP, C.c_int32, C.c_int32, VP]),
+    "ora_bfs_multi": (I64, [VP, VP, C.c_int32, VP, C.c_int32, C.c_int32, VP]),
+    "ora_bfs_ref_graph": (I, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, U64, U64, VP, U64, VP, U64, VP,
+                              VP, VP, VP]),
     "ora_dep_build": (I, [VP, U64, VP, VP, C.c_int32, U64]),
     "ora_dep_probe": (None, [VP, U64, VP, I64, I, VP]),
 }
@@ -233,6 +236,34 @@ def bfs(rowptr: np.ndarray, col: np.ndarray, src: int):
     level = np.empty(V, dtype=np.uint32)
     n = int(lib.ora_bfs(_p(rowptr), _p(col) if col.size else None, V, src, _p(level)))
     return level, n
+
+
+def bfs_multi(rowptr: np.ndarray, col: np.ndarray, sources: np.ndarray, max_depth: int):
+    """Multi-source BFS limited to max_depth top-down levels: (level u32[V], number reached)."""
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    col = np.ascontiguousarray(col, dtype=np.int32)
+    sources = np.ascontiguousarray(sources, dtype=np.int32)
+    V = rowptr.size - 1
+    level = np.empty(V, dtype=np.uint32)
+    n = int(lib.ora_bfs_multi(_p(rowptr), _p(col) if col.size else None, V, _p(sources) if sources.size else None,
+                              sources.size, max_depth, _p(level)))
+    return level, n
+
+
+def bfs_ref_graph(V: int, degree: int, nsrc: int, dst_local_pct: int, H: int, seed: int, col_addr: int,
+                  col_home, level_addr: int, level_home, mask: int):
+    """bfs.cu:354-409: (rowptr, col, work_side, sources), or None when a hot pool is short."""
+    rowptr = np.empty(V + 1, dtype=np.int32)
+    col = np.empty(V * degree, dtype=np.int32)
+    ws = np.empty(V, dtype=np.uint8)
+    src = np.empty(max(nsrc, 1), dtype=np.int32)
+    ch = None if col_home is None else np.ascontiguousarray(col_home, dtype=np.uint8)
+    lh = None if level_home is None else np.ascontiguousarray(level_home, dtype=np.uint8)
+    rc = lib.ora_bfs_ref_graph(V, degree, nsrc, dst_local_pct, H, seed, col_addr, None if ch is None else _p(ch),
+                               level_addr, None if lh is None else _p(lh), mask, _p(rowptr), _p(col), _p(ws), _p(src))
+    if rc != 0:
+        return None
+    return rowptr, col, ws, src[:nsrc]
 
 
 def dep_build(slots: int, keys: np.ndarray, nexts: np.ndarray, seed: int) -> np.ndarray:

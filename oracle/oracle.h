@@ -68,6 +68,13 @@ int64_t ora_rmat_csr(int scale, int edge_factor, double a, double b, double c, u
                      int32_t *col);
 /* Serial FIFO-queue BFS; returns the number of reached vertices. */
 int64_t ora_bfs(const int32_t *rowptr, const int32_t *col, int32_t V, int32_t src, uint32_t *level);
+/* The reference's workload: multi-source BFS limited to max_depth levels over a directed graph
+ * (bfs.cu:151-252, 449-491), and its hot-pool graph (bfs.cu:354-409). */
+int64_t ora_bfs_multi(const int32_t *rowptr, const int32_t *col, int32_t V, const int32_t *src, int32_t nsrc,
+                      int32_t max_depth, uint32_t *level);
+int ora_bfs_ref_graph(int32_t V, int32_t degree, int32_t nsrc, int32_t dst_local_pct, int32_t H, uint64_t seed,
+                      uint64_t col_addr, const uint8_t *col_home, uint64_t level_addr, const uint8_t *level_home,
+                      uint64_t mask, int32_t *rowptr, int32_t *col, uint8_t *work_side, int32_t *src);
 
 /* The reference's dependent-probe workload (applications/hash/src/hash_probe_dep.cu).
  * ora_dep_build: table[2*slots] {key, next}, EMPTY -1, serial insertion (HASH.cu:232-241) in

@@ -42,3 +42,28 @@ def test_mix32_generators_match_oracle():
                                           ora.mix32_f32(n, seed, mod, off).view(np.uint32))
     A, x = gen.gemv_mix32_inputs(4, 1024)
     np.testing.assert_array_equal(x, ora.mix32_f32(1024, 4242 + 0x9E37))
+
+
+def test_bfs_ref_graph_product_matches_oracle():
+    import ctypes as C
+    from l2domain_amd import _lib
+    rng = np.random.default_rng(4)
+    for V, deg, nsrc, dl, H, maps in ((9000, 3, 50, 95, 1024, True), (5000, 8, 20, 0, 1024, False)):
+        col_addr, level_addr = 0x7E0000000000 + 8192 * 7, 0x7E8000000000 + 4096 * 3
+        ch = rng.integers(0, 2, size=(V * deg * 4) // (2 << 20) + 2, dtype=np.uint8) if maps else None
+        lh = rng.integers(0, 2, size=(V * 4) // (2 << 20) + 2, dtype=np.uint8) if maps else None
+        mask = int(_lib.lib.xd_home_mask())
+        ref = ora.bfs_ref_graph(V, deg, nsrc, dl, H, 8201, col_addr, ch, level_addr, lh, mask)
+        rowptr = np.empty(V + 1, dtype=np.int32)
+        col = np.empty(V * deg, dtype=np.int32)
+        ws = np.empty(V, dtype=np.uint8)
+        src = np.empty(nsrc, dtype=np.int32)
+        rc = _lib.lib.xd_bfs_ref_graph(V, deg, nsrc, dl, H, 8201, col_addr, None if ch is None else ch.ctypes.data,
+                                       level_addr, None if lh is None else lh.ctypes.data, rowptr.ctypes.data,
+                                       col.ctypes.data, ws.ctypes.data, src.ctypes.data)
+        if ref is None:
+            assert rc == _lib.XD_ERR_UNSUPPORTED
+            continue
+        assert rc == 0
+        for a, b in zip((rowptr, col, ws, src), ref):
+            np.testing.assert_array_equal(a, b)

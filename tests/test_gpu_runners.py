@@ -94,8 +94,10 @@ def test_hash_runner(tmp_path, workload):
     assert (tmp_path / "x.csv").read_text().splitlines()[0].startswith("K,Q,C,effective_load,L,h,H,baseline_ms")
 
 
-def test_bfs_runner(tmp_path):
-    rc, out, err = run("xd_bfs_run", 1 << 16, 32, 2, 0, 100, 0, 2, 8201, csv=tmp_path / "b.csv")
+@pytest.mark.parametrize("args", [(65536, 8, 128, 2, 95, 4096, 1, 8201),  # the reference's quick preset
+                                  ("--workload=rmat", 1 << 16, 32, 2, 0, 100, 0, 2, 8201)])
+def test_bfs_runner(tmp_path, args):
+    rc, out, err = run("xd_bfs_run", *args, csv=tmp_path / "b.csv")
     assert rc == 0, out + err
     line = next(l for l in out.splitlines() if l.startswith("visited="))
     f = line.replace("=", " ").split()  # awk -F'[ =]' ... $2, $4, $6, $8

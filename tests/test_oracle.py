@@ -412,3 +412,73 @@ def test_gemv_mix32_init_known_answers():
     assert np.isin(vals, grid).all()
     xi = ora.mix32_f32(1 << 12, 7 + 0x9E37, 7, 3)
     assert xi.min() == -3 and xi.max() == 3
+
+
+def _sp_multi(rowptr, col, sources, max_depth):
+    from scipy.sparse import csr_matrix
+    from scipy.sparse.csgraph import shortest_path
+    V = rowptr.size - 1
+    g = csr_matrix((np.ones(col.size), col, rowptr), shape=(V, V))
+    d = np.atleast_2d(shortest_path(g, directed=True, unweighted=True, indices=np.unique(sources))).min(axis=0)
+    out = np.full(V, 0xFFFFFFFF, dtype=np.uint32)
+    ok = np.isfinite(d) & (d <= max_depth)
+    out[ok] = d[ok].astype(np.uint32)
+    return out
+
+
+def test_bfs_multi_oracle_matches_scipy():
+    """bfs.cu:151-252, 449-491: all sources at 0, max_depth top-down levels over a directed
+    graph. Pinned by scipy's multi-source unweighted shortest paths, cut at max_depth."""
+    rng = np.random.default_rng(11)
+    for V, m, nsrc in ((1, 0, 1), (50, 200, 3), (700, 2100, 9), (3000, 9000, 40)):
+        u = rng.integers(0, V, size=m)
+        v = rng.integers(0, V, size=m)
+        order = np.argsort(u, kind="stable")
+        col = v[order].astype(np.int32)
+        rowptr = np.zeros(V + 1, dtype=np.int32)
+        np.add.at(rowptr, u + 1, 1)
+        rowptr = np.cumsum(rowptr).astype(np.int32)
+        src = rng.integers(0, V, size=nsrc).astype(np.int32)  # duplicates allowed
+        for depth in (0, 1, 2, 5, 1000):
+            level, n = ora.bfs_multi(rowptr, col, src, depth)
+            ref = _sp_multi(rowptr, col, src, depth)
+            np.testing.assert_array_equal(level, ref)
+            assert n == int((ref != 0xFFFFFFFF).sum())
+
+
+def test_bfs_ref_graph_structure():
+    """bfs.cu:354-409: pools are the first H vertices per side whose row and level homes
+    agree; every vertex has exactly `degree` neighbours, all from one pool (the other pool
+    for the last cross_per_side hot vertices of each pool, whose work side flips); sources
+    alternate hot0, hot1 from the start of the pools."""
+    rng = np.random.default_rng(2)
+    V, deg, nsrc, dst_local, H, seed = 6000, 5, 37, 90, 1024, 8201
+    col_addr, level_addr = 0x7F0000000000 + 3 * 8192, 0x7F4000000000 + 5 * 4096
+    ch = rng.integers(0, 2, size=(V * deg * 4) // (2 << 20) + 2, dtype=np.uint8)
+    lh = rng.integers(0, 2, size=(V * 4) // (2 << 20) + 2, dtype=np.uint8)
+    g = ora.bfs_ref_graph(V, deg, nsrc, dst_local, H, seed, col_addr, ch, level_addr, lh, 0)
+    assert g is not None
+    rowptr, col, work_side, src = g
+
+    def side(addr, base, attr):
+        return ((addr >> 13) & 1) ^ int(attr[(addr >> 21) - (base >> 21)])
+
+    rs = [side(col_addr + v * deg * 4, col_addr, ch) for v in range(V)]
+    ds = [side(level_addr + v * 4, level_addr, lh) for v in range(V)]
+    pools = [[v for v in range(V) if rs[v] == ds[v] == s][:H] for s in (0, 1)]
+    assert all(len(p) == H for p in pools)
+    cross = H * (100 - dst_local) // 100
+    crossers = {p[H - 1 - i]: s for s, p in enumerate(pools) for i in range(cross)}
+    np.testing.assert_array_equal(rowptr, np.arange(V + 1) * deg)
+    sets = [set(p) for p in pools]
+    for v in range(V):
+        want = rs[v] ^ (1 if v in crossers else 0)
+        assert set(col[v * deg:(v + 1) * deg].tolist()) <= sets[want]
+        assert work_side[v] == want
+    assert [int(x) for x in src] == [pools[i & 1][(i // 2) % H] for i in range(nsrc)]
+    # neighbour draws use splitmix64(seed, v * degree + j) mod H
+    v, j = 123, 4
+    want = rs[v] ^ (1 if v in crossers else 0)
+    assert col[v * deg + j] == pools[want][ora.splitmix64(seed, v * deg + j) % H]
+    # a pool that cannot be filled is reported
+    assert ora.bfs_ref_graph(V, deg, nsrc, dst_local, V, seed, col_addr, ch, level_addr, lh, 0) is None

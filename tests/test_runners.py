@@ -35,3 +35,8 @@ def test_runner_argument_checks():
     assert r.returncode == 2
     r = subprocess.run([str(BIN / "xd_hist_run"), "4096"], capture_output=True, text=True, timeout=60)
     assert r.returncode == 2  # 4096 MiB of words would overflow the u32 byte counts
+
+
+def test_bfs_runner_rejects_unknown_workload():
+    r = subprocess.run([str(BIN / "xd_bfs_run"), "--workload=grid"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2

@@ -12,18 +12,25 @@
 //     (449-491); swapped = each side consumes the other side's frontier (invert, :258).
 //
 // MI355X design.
-//   claims: a visited bitmap (V bits, resident in every XCD's L2) filters with a plain load,
-//     then a 64-bit atomicOr decides; the winner writes level[dst] = depth + 1.
-//   expansion: a group of G lanes per frontier vertex walks its adjacency list (G = the
-//     power of two nearest the mean degree, at most 64), so the list is read in coalesced
-//     runs; winners are appended with one atomicAdd per wave and target queue (ballot +
-//     mbcnt), no LDS staging and no overflow.
-//   queues: two per level (one per I/O die, chosen by work_side[v]); XCD-aware: the
-//     workgroups of die d (XCDs 4d..4d+3) consume queue d, and a winner goes to the queue of
-//     its own work side; rotated: die d consumes queue 1 - d; oblivious: one queue, every
-//     workgroup. Three queue pairs rotate, and the kernel of level k clears the counters of
-//     the pair level k + 1 will fill, so the whole search is enqueued without host round
-//     trips and without memsets.
+//   claims: a visited bitmap (V bits, resident in every XCD's L2) filters with a plain load
+//     (it holds every vertex claimed in earlier levels); a compare-and-swap of level[dst]
+//     from 0xFFFFFFFF to depth + 1 decides, and the winner sets the bitmap bit with an
+//     atomic whose result it does not wait for. (A 64-bit atomicOr on the bitmap as the
+//     claim put 512 vertices on each contended line and made every claim slow.)
+//   expansion: a group of G lanes per frontier vertex walks its adjacency list, four
+//     neighbours per lane and step with their loads issued together (G = the power of two
+//     nearest a quarter of the mean degree, at most 64).
+//   appends: winners are staged in a per-wave LDS buffer (ballot + mbcnt) and flushed 256 at
+//     a time with one atomicAdd; each frontier is split into 8 sub-queues, one per producing
+//     XCD slot (workgroup mod 8), so the flushes spread over 8 counters. A counter taking one
+//     atomic per wave and step was the bound of an earlier version (memory-side atomics on
+//     one address serialise).
+//   queues: two frontiers per level (one per I/O die, chosen by work_side[v]); XCD-aware:
+//     the workgroups of die d (XCDs 4d..4d+3) consume frontier d, and a winner goes to the
+//     frontier of its own work side; rotated: die d consumes frontier 1 - d; oblivious: one
+//     frontier, every workgroup. Three frontier pairs rotate, and the kernel of level k clears
+//     the counters of the pair level k + 1 will fill, so the whole search is enqueued without
+//     host round trips and without memsets.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -37,19 +44,24 @@ constexpr int kMThreads = 256;
 constexpr int kMWaves = kMThreads / kWave;
 constexpr int kMGrid = 2048;  // level kernels (a multiple of 8)
 
+constexpr int kMSub = kNumXcd;   // sub-queues per frontier (one per producing XCD slot)
+constexpr int kMStage = 256;     // staged winners per wave and frontier before a flush
+constexpr int kMUnroll = 4;      // neighbours per lane and step
+
 struct MultiLayout {
     size_t visited, queues, counts, total;
 };
 
 static size_t m_a256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// queue q of level slot l (0..2), frontier f (0..1), sub-queue k (0..7): index (l*2+f)*8+k
 static MultiLayout multi_layout(int32_t V) {
     MultiLayout L;
     const size_t words = ((size_t)V + 63) / 64;
     L.visited = 0;
     L.queues = m_a256(L.visited + words * 8);
-    L.counts = m_a256(L.queues + (size_t)6 * (size_t)V * 4);  // 3 levels x 2 dies
-    L.total = L.counts + 256;
+    L.counts = m_a256(L.queues + (size_t)6 * kMSub * (size_t)V * 4);
+    L.total = L.counts + 6 * kMSub * 4;
     return L;
 }
 
@@ -59,29 +71,10 @@ __global__ void __launch_bounds__(kMThreads) multi_init_kernel(uint32_t *level, 
     const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (int64_t i = i0; i < V; i += stride) level[i] = kMUnv;
     for (int64_t i = i0; i < ((int64_t)V + 63) / 64; i += stride) visited[i] = 0ull;
-    if (i0 < 6) counts[i0] = 0u;
+    if (i0 < 6 * kMSub) counts[i0] = 0u;
 }
 
-// Appends v (for the lanes with take == true) to queue[side] with one atomic per wave and side.
-__device__ __forceinline__ void multi_append(bool take, uint32_t side, int32_t v, int32_t *q0, int32_t *q1,
-                                             uint32_t *cnt) {
-    const int lane = (int)__lane_id();
-#pragma unroll
-    for (uint32_t s = 0; s < 2; ++s) {
-        const uint64_t m = __ballot(take && side == s);
-        if (m == 0) continue;
-        const int leader = __ffsll((long long)m) - 1;
-        uint32_t base = 0;
-        if (lane == leader) base = atomicAdd(&cnt[s], (uint32_t)__popcll(m));
-        base = __shfl(base, leader);
-        if (take && side == s) {
-            const uint32_t pos = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
-            (s == 0 ? q0 : q1)[pos] = v;
-        }
-    }
-}
-
-// Claims v at distance lvl: true for the one thread that set its visited bit.
+// Claims v: true for the one thread that set its visited bit.
 __device__ __forceinline__ bool multi_claim(unsigned long long *visited, int32_t v) {
     const unsigned long long bit = 1ull << (v & 63);
     unsigned long long *w = visited + (v >> 6);
@@ -89,34 +82,84 @@ __device__ __forceinline__ bool multi_claim(unsigned long long *visited, int32_t
     return (atomicOr(w, bit) & bit) == 0ull;
 }
 
+// Per-wave staging of the winners of one level. Every call is made by the whole wave.
+struct Stager {
+    int32_t *buf;      // this wave's LDS buffer, kMStage entries per frontier
+    uint32_t fill[2];  // wave-uniform
+    int32_t *q[2];     // the sub-queue of each frontier this workgroup fills
+    uint32_t *cnt[2];
+
+    __device__ __forceinline__ void flush(int f) {
+        const uint32_t n = fill[f];
+        if (n == 0) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the staged entries are visible to the wave
+        const int lane = (int)__lane_id();
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(cnt[f], n);
+        base = __shfl(base, 0);
+        for (uint32_t k = (uint32_t)lane; k < n; k += kWave) q[f][base + k] = buf[f * kMStage + k];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // read before the buffer is refilled
+        fill[f] = 0;
+    }
+    __device__ __forceinline__ void append(bool take, uint32_t f_of, int32_t v) {
+        const int lane = (int)__lane_id();
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            const uint64_t m = __ballot(take && f_of == (uint32_t)f);
+            if (m == 0) continue;
+            const uint32_t c = (uint32_t)__popcll(m);
+            if (fill[f] + c > (uint32_t)kMStage) flush(f);
+            if (take && f_of == (uint32_t)f) buf[f * kMStage + fill[f] + (uint32_t)__popcll(m & ((1ull << lane) - 1ull))] = v;
+            fill[f] += c;
+        }
+    }
+};
+
+// Position i of a frontier made of kMSub sub-queues (counts c[0..7], concatenated in order).
+__device__ __forceinline__ int32_t sub_index(uint32_t i, const uint32_t *pre, const int32_t *q0, int32_t V) {
+    int k = 0;
+#pragma unroll
+    for (int j = 1; j < kMSub; ++j) k += i >= pre[j] ? 1 : 0;
+    return q0[(size_t)k * V + (i - pre[k])];
+}
+
 __global__ void __launch_bounds__(kMThreads)
 multi_seed_kernel(const int32_t *__restrict__ sources, int32_t nsrc, const uint8_t *__restrict__ work_side, int routed,
                   uint32_t *__restrict__ level, unsigned long long *visited, int32_t *queues, uint32_t *counts,
                   int32_t V) {
+    __shared__ int32_t sbuf[kMWaves][2 * kMStage];
+    const int wave = (int)threadIdx.x / kWave;
+    const int k = (int)blockIdx.x % kMSub;
+    Stager st{sbuf[wave], {0u, 0u}, {queues + (size_t)k * V, queues + (size_t)(kMSub + k) * V},
+              {counts + k, counts + kMSub + k}};
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     bool take = false;
     int32_t v = 0;
-    uint32_t side = 0;
+    uint32_t f = 0;
     if (i < nsrc) {
         v = sources[i];
         take = multi_claim(visited, v);
         if (take) {
             level[v] = 0u;
-            side = routed ? (uint32_t)(work_side[v] & 1u) : 0u;
+            f = routed ? (uint32_t)(work_side[v] & 1u) : 0u;
         }
     }
-    multi_append(take, side, v, queues, queues + V, counts);
+    st.append(take, f, v);
+    st.flush(0);
+    st.flush(1);
 }
 
-// One top-down level: consumes queue pair `cur`, fills pair (cur + 1) % 3 and clears the
-// counters of pair (cur + 2) % 3. lg = log2 of the lanes per frontier vertex.
+// One top-down level: consumes frontier pair `cur`, fills pair (cur + 1) % 3 and clears the
+// counters of pair (cur + 2) % 3. A group of G = 2^lg lanes takes one frontier vertex, and
+// each lane handles kMUnroll neighbours per step with their loads issued together.
 __global__ void __launch_bounds__(kMThreads)
 multi_level_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict__ col,
                    const uint8_t *__restrict__ work_side, uint32_t *__restrict__ level, unsigned long long *visited,
                    int32_t *queues, uint32_t *counts, int32_t V, uint32_t depth, int lg, int mode, int cur) {
+    __shared__ int32_t sbuf[kMWaves][2 * kMStage];
     const int nxt = (cur + 1) % 3, clr = (cur + 2) % 3;
     const int b = (int)blockIdx.x, grid = (int)gridDim.x;
-    if (b == 0 && threadIdx.x < 2) counts[2 * clr + threadIdx.x] = 0u;
+    if (b == 0 && threadIdx.x < 2 * kMSub) counts[2 * kMSub * clr + threadIdx.x] = 0u;
     const bool routed = mode != XD_MODE_OBLIVIOUS;
     int rank, nwg;
     uint32_t side = 0;
@@ -128,12 +171,23 @@ multi_level_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict
         nwg = grid / 2;
         side = wg_die(b) ^ (mode == XD_MODE_ROTATED ? 1u : 0u);
     }
-    const uint32_t n = counts[2 * cur + side];
-    const int32_t *q = queues + (size_t)(2 * cur + side) * V;
-    int32_t *n0 = queues + (size_t)(2 * nxt) * V, *n1 = n0 + V;
-    uint32_t *ncnt = counts + 2 * nxt;
+    // the frontier this workgroup consumes: kMSub sub-queues, prefix sums of their lengths
+    const uint32_t *ccnt = counts + (size_t)(2 * cur + side) * kMSub;
+    const int32_t *cq = queues + (size_t)(2 * cur + side) * kMSub * V;
+    uint32_t pre[kMSub];
+    uint32_t n = 0;
+#pragma unroll
+    for (int k = 0; k < kMSub; ++k) {
+        pre[k] = n;
+        n += ccnt[k];
+    }
+    const int wave = (int)threadIdx.x / kWave;
+    const int sq = b % kMSub;  // the sub-queue this workgroup fills
+    Stager st{sbuf[wave], {0u, 0u},
+              {queues + ((size_t)(2 * nxt) * kMSub + sq) * V, queues + ((size_t)(2 * nxt + 1) * kMSub + sq) * V},
+              {counts + (size_t)(2 * nxt) * kMSub + sq, counts + (size_t)(2 * nxt + 1) * kMSub + sq}};
     const int G = 1 << lg;
-    const int lane = (int)__lane_id(), wave = (int)threadIdx.x / kWave;
+    const int lane = (int)__lane_id();
     const int sub = lane & (G - 1);
     const uint32_t per_wave = (uint32_t)(kWave >> lg);  // frontier vertices per wave and pass
     const uint32_t stride = (uint32_t)nwg * kMWaves * per_wave;
@@ -141,29 +195,51 @@ multi_level_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict
         const uint32_t i = base + (uint32_t)(lane >> lg);
         int32_t beg = 0, end = 0;
         if (i < n) {
-            const int32_t v = q[i];
+            const int32_t v = sub_index(i, pre, cq, V);
             beg = rowptr[v];
             end = rowptr[v + 1];
         }
-        // the wave walks the longest list of its vertices; every lane takes part in the
-        // appends, so the ballots see the whole wave
+        // the wave walks the longest list of its vertices in lock step, so that every lane
+        // takes part in the ballots and flushes
         int32_t len = end - beg;
-        for (int off = kWave / 2; off >= G; off >>= 1) len = max(len, __shfl_xor(len, off));
-        for (int32_t j = sub; j < len; j += G) {
-            bool take = false;
-            int32_t dst = 0;
-            uint32_t ds = 0;
-            if (beg + j < end) {
-                dst = col[beg + j];
-                take = multi_claim(visited, dst);
-                if (take) {
-                    level[dst] = depth + 1u;
-                    ds = routed ? (uint32_t)(work_side[dst] & 1u) : 0u;
+        for (int off = kWave / 2; off >= 1; off >>= 1) len = max(len, __shfl_xor(len, off));
+        for (int32_t jb = 0; jb < len; jb += G * kMUnroll) {
+            int32_t dst[kMUnroll];
+            unsigned long long w[kMUnroll];
+#pragma unroll
+            for (int u = 0; u < kMUnroll; ++u) {
+                const int32_t e = beg + jb + sub + u * G;
+                dst[u] = e < end ? col[e] : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < kMUnroll; ++u) w[u] = dst[u] >= 0 ? visited[dst[u] >> 6] : ~0ull;
+            // the claim is a compare-and-swap on the vertex's own level entry (16 vertices per
+            // line, where a bitmap word shares its line with 512 and serialises), and all
+            // claims of a step are issued before any result is used
+            uint32_t old[kMUnroll];
+#pragma unroll
+            for (int u = 0; u < kMUnroll; ++u) {
+                old[u] = 0u;
+                if (dst[u] >= 0 && !(w[u] & (1ull << (dst[u] & 63))))
+                    old[u] = atomicCAS(level + dst[u], kMUnv, depth + 1u);
+            }
+            bool take[kMUnroll];
+            uint32_t f[kMUnroll];
+#pragma unroll
+            for (int u = 0; u < kMUnroll; ++u) {
+                take[u] = old[u] == kMUnv;
+                f[u] = 0;
+                if (take[u]) {
+                    atomicOr(visited + (dst[u] >> 6), 1ull << (dst[u] & 63));  // filter of later levels; no return
+                    if (routed) f[u] = (uint32_t)(work_side[dst[u]] & 1u);
                 }
             }
-            multi_append(take, ds, dst, n0, n1, ncnt);
+#pragma unroll
+            for (int u = 0; u < kMUnroll; ++u) st.append(take[u], f[u], dst[u]);
         }
     }
+    st.flush(0);
+    st.flush(1);
 }
 
 }  // namespace xd
@@ -197,8 +273,8 @@ int xd_bfs_multi(const int32_t *rowptr, const int32_t *col, int32_t num_vertices
     int32_t *queues = reinterpret_cast<int32_t *>(ws + L.queues);
     uint32_t *counts = reinterpret_cast<uint32_t *>(ws + L.counts);
     const int routed = mode != XD_MODE_OBLIVIOUS ? 1 : 0;
-    // lanes per frontier vertex: the power of two nearest the mean degree, in [1, 64]
-    const double mean = (double)nnz / (double)V;
+    // lanes per frontier vertex: the power of two nearest mean degree / kMUnroll, in [1, 64]
+    const double mean = (double)nnz / (double)V / kMUnroll;
     int lg = 0;
     while (lg < 6 && (double)(2 << lg) <= mean * 1.5) ++lg;
 

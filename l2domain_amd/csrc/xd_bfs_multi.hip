@@ -17,9 +17,9 @@
 //     from 0xFFFFFFFF to depth + 1 decides, and the winner sets the bitmap bit with an
 //     atomic whose result it does not wait for. (A 64-bit atomicOr on the bitmap as the
 //     claim put 512 vertices on each contended line and made every claim slow.)
-//   expansion: a group of G lanes per frontier vertex walks its adjacency list, four
-//     neighbours per lane and step with their loads issued together (G = the power of two
-//     nearest a quarter of the mean degree, at most 64).
+//   expansion: a group of G lanes per frontier vertex walks its adjacency list, eight
+//     neighbours per lane and step with their loads and claims issued together (G = the
+//     power of two nearest an eighth of the mean degree, at most 64).
 //   appends: winners are staged in a per-wave LDS buffer (ballot + mbcnt) and flushed 256 at
 //     a time with one atomicAdd; each frontier is split into 8 sub-queues, one per producing
 //     XCD slot (workgroup mod 8), so the flushes spread over 8 counters. A counter taking one
@@ -46,7 +46,7 @@ constexpr int kMGrid = 2048;  // level kernels (a multiple of 8)
 
 constexpr int kMSub = kNumXcd;   // sub-queues per frontier (one per producing XCD slot)
 constexpr int kMStage = 256;     // staged winners per wave and frontier before a flush
-constexpr int kMUnroll = 4;      // neighbours per lane and step
+constexpr int kMUnroll = 8;      // neighbours per lane and step
 
 struct MultiLayout {
     size_t visited, queues, counts, total;

@@ -293,6 +293,21 @@ int xd_dep_queries(int32_t *queries, int32_t Q, const int32_t *keys, int32_t K, 
 int xd_dep_probe(const void *table, uint64_t slots, const int32_t *queries, uint64_t n, int chain_len,
                  int32_t *out, int mode, const uint8_t *home_attr, void *stream);
 
+/* The reference's routed form of the dependent probe, with the routing as its own step:
+ * xd_dep_route (device) partitions the queries, in order, into two lists of {key, query id}
+ * by the I/O die homing each query's first slot (the near/far lists the reference builds on
+ * the host, HASH.cu:244-270, outside its timed region); route is a device buffer of
+ * xd_dep_route_bytes(n) bytes, 16-byte aligned. xd_dep_probe_routed (device) runs
+ * probe_dep_sa (HASH.cu:85-116): die d probes list d (XD_MODE_AWARE) or list 1 - d
+ * (XD_MODE_ROTATED; XD_MODE_OBLIVIOUS: every workgroup takes both lists) and writes
+ * out[query id] exactly as xd_dep_probe does. n < 2^31. The route stays valid for the same
+ * table, queries and home map. */
+size_t xd_dep_route_bytes(uint64_t n);
+int xd_dep_route(const void *table, uint64_t slots, const int32_t *queries, uint64_t n, const uint8_t *home_attr,
+                 void *route, size_t route_bytes, void *stream);
+int xd_dep_probe_routed(const void *table, uint64_t slots, const void *route, uint64_t n, int chain_len,
+                        int32_t *out, int mode, void *stream);
+
 /* ------------------------------------------------------------------------------------ */
 /* BFS over an undirected CSR graph                                                       */
 /* ------------------------------------------------------------------------------------ */

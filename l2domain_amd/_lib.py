@@ -99,6 +99,9 @@ SIGNATURES: dict[str, tuple] = {
     "xd_dep_build": (I, [VP, U64, VP, VP, C.c_int32, U64]),
     "xd_dep_queries": (I, [VP, C.c_int32, VP, C.c_int32, C.c_int32, C.c_int32, U64]),
     "xd_dep_probe": (I, [VP, U64, VP, U64, I, VP, I, VP, VP]),
+    "xd_dep_route_bytes": (SZ, [U64]),
+    "xd_dep_route": (I, [VP, U64, VP, U64, VP, VP, SZ, VP]),
+    "xd_dep_probe_routed": (I, [VP, U64, VP, U64, I, VP, I, VP]),
     "xd_bfs_workspace_size": (SZ, [C.c_int32, I64]),
     "xd_bfs_route_bytes": (SZ, [C.c_int32]),
     "xd_bfs_route": (I, [VP, VP, C.c_int32, I64, VP, VP, SZ, VP]),

@@ -267,6 +267,171 @@ dep_probe_kernel(const int2 *__restrict__ table, uint32_t mask, const int32_t *_
     for_each_owned(w, n, filter, queues[threadIdx.x / kWave], key_of, keep, body);
 }
 
+// Routed dependent probe: the reference's per-side query lists (HASH.cu:244-270, built on the
+// host there, outside the timed region) built on the device by an order-preserving partition
+// of the queries by the die homing their first slot; probe_dep_sa (:85-116) is then a probe
+// in which die d consumes list d (aware) or list 1 - d (rotated) and scatters out[qid].
+// Route buffer: {uint64 n0, uint64 n} | per-block die-1 counts (their exclusive prefix after
+// the scan) | int2 entries {key, qid}: die-0 list [0, n0), die-1 list [n0, n), each in query
+// order.
+constexpr int kRouteBlock = 4096;  // queries per partition block
+constexpr int kRoutePer = kRouteBlock / kHashThreads;
+constexpr int kScanThreads = 1024;
+
+struct RouteLayout {
+    size_t bcnt, entries, total;
+    uint64_t nblocks;
+};
+
+static RouteLayout route_layout(uint64_t n) {
+    RouteLayout L;
+    L.nblocks = (n + kRouteBlock - 1) / kRouteBlock;
+    L.bcnt = 256;
+    L.entries = (L.bcnt + 4 * L.nblocks + 255) & ~(size_t)255;
+    L.total = L.entries + 8 * n;
+    return L;
+}
+
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t *red) {
+    v = wave_sum_u32(v);
+    const int wave = (int)threadIdx.x / kWave;
+    if (lane_id() == 0) red[wave] = v;
+    __syncthreads();
+    uint32_t t = 0;
+    for (int w = 0; w < (int)blockDim.x / kWave; ++w) t += red[w];
+    __syncthreads();
+    return t;
+}
+
+__global__ void __launch_bounds__(kHashThreads)
+route_count_kernel(uint32_t mask, const int32_t *__restrict__ queries, uint64_t n, HomeMap home, uint64_t base,
+                   uint32_t *__restrict__ bcnt) {
+    __shared__ uint8_t lattr[kLdsPages];
+    __shared__ uint32_t red[kHashThreads / kWave];
+    const SlotHome sh = stage_home(home, base, ((uint64_t)mask + 1) * sizeof(int2), lattr, true);
+    const uint64_t i0 = (uint64_t)blockIdx.x * kRouteBlock;
+    uint32_t c1 = 0;
+#pragma unroll
+    for (int j = 0; j < kRoutePer; ++j) {
+        const uint64_t i = i0 + (uint64_t)j * kHashThreads + threadIdx.x;
+        if (i < n) c1 += sh(base + (uint64_t)(mix32d((uint32_t)queries[i]) & mask) * sizeof(int2));
+    }
+    const uint32_t t = block_sum_u32(c1, red);
+    if (threadIdx.x == 0) bcnt[blockIdx.x] = t;
+}
+
+// One workgroup: exclusive prefix of the per-block die-1 counts, in place; header = {n0, n}.
+__global__ void __launch_bounds__(kScanThreads) route_scan_kernel(uint32_t *bcnt, uint64_t nblocks, uint64_t n,
+                                                                 unsigned long long *header) {
+    __shared__ uint32_t wsum[kScanThreads / kWave];
+    __shared__ uint64_t carry_s;
+    if (threadIdx.x == 0) carry_s = 0;
+    __syncthreads();
+    const int lane = lane_id(), wave = (int)threadIdx.x / kWave;
+    for (uint64_t c0 = 0; c0 < nblocks; c0 += kScanThreads) {
+        const uint64_t i = c0 + threadIdx.x;
+        const uint32_t v = i < nblocks ? bcnt[i] : 0u;
+        uint32_t incl = v;  // inclusive scan inside the wave
+        for (int off = 1; off < kWave; off <<= 1) {
+            const uint32_t o = __shfl_up(incl, off);
+            if (lane >= off) incl += o;
+        }
+        if (lane == kWave - 1) wsum[wave] = incl;
+        __syncthreads();
+        uint32_t before = 0, total = 0;
+        for (int w = 0; w < kScanThreads / kWave; ++w) {
+            if (w < wave) before += wsum[w];
+            total += wsum[w];
+        }
+        const uint64_t carry = carry_s;
+        if (i < nblocks) bcnt[i] = (uint32_t)(carry + before + incl - v);
+        __syncthreads();
+        if (threadIdx.x == 0) carry_s = carry + total;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        header[0] = n - carry_s;
+        header[1] = n;
+    }
+}
+
+__global__ void __launch_bounds__(kHashThreads)
+route_scatter_kernel(uint32_t mask, const int32_t *__restrict__ queries, uint64_t n, HomeMap home, uint64_t base,
+                     const uint32_t *__restrict__ bcnt, const unsigned long long *__restrict__ header,
+                     int2 *__restrict__ entries) {
+    __shared__ uint8_t lattr[kLdsPages];
+    __shared__ uint32_t w0[kHashThreads / kWave], w1[kHashThreads / kWave];
+    const SlotHome sh = stage_home(home, base, ((uint64_t)mask + 1) * sizeof(int2), lattr, true);
+    const uint64_t b = blockIdx.x, i0 = b * kRouteBlock;
+    const uint64_t n0 = header[0];
+    const uint64_t off1 = bcnt[b], off0 = i0 - off1;
+    const int lane = lane_id(), wave = (int)threadIdx.x / kWave;
+    const uint64_t lt = (1ull << lane) - 1ull;
+    uint64_t r0 = 0, r1 = 0;  // entries of each list written by the earlier slabs of this block
+    for (int j = 0; j < kRoutePer; ++j) {
+        const uint64_t i = i0 + (uint64_t)j * kHashThreads + threadIdx.x;
+        const bool valid = i < n;
+        const int32_t key = valid ? queries[i] : 0;
+        const uint32_t d = valid ? sh(base + (uint64_t)(mix32d((uint32_t)key) & mask) * sizeof(int2)) : 0u;
+        const uint64_t m1 = __ballot(valid && d == 1u), m0 = __ballot(valid && d == 0u);
+        if (lane == 0) {
+            w0[wave] = (uint32_t)__builtin_popcountll(m0);
+            w1[wave] = (uint32_t)__builtin_popcountll(m1);
+        }
+        __syncthreads();
+        uint32_t p0 = 0, p1 = 0, t0 = 0, t1 = 0;
+        for (int w = 0; w < kHashThreads / kWave; ++w) {
+            if (w < wave) {
+                p0 += w0[w];
+                p1 += w1[w];
+            }
+            t0 += w0[w];
+            t1 += w1[w];
+        }
+        if (valid) {
+            const uint64_t pos = d ? n0 + off1 + r1 + p1 + (uint64_t)__builtin_popcountll(m1 & lt)
+                                   : off0 + r0 + p0 + (uint64_t)__builtin_popcountll(m0 & lt);
+            entries[pos] = make_int2(key, (int32_t)i);
+        }
+        r0 += t0;
+        r1 += t1;
+        __syncthreads();
+    }
+}
+
+__global__ void __launch_bounds__(kHashThreads)
+dep_probe_routed_kernel(const int2 *__restrict__ table, uint32_t mask, const int2 *__restrict__ entries,
+                        const unsigned long long *__restrict__ header, int chain_len, int32_t *__restrict__ out,
+                        int mode) {
+    const uint64_t n0 = header[0], n = header[1];
+    const int b = (int)blockIdx.x;
+    uint64_t first, end, rank, nwg;
+    if (mode == XD_MODE_OBLIVIOUS) {
+        first = 0;
+        end = n;
+        rank = (uint64_t)b;
+        nwg = gridDim.x;
+    } else {
+        const uint32_t die = wg_die(b);
+        const uint32_t list = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
+        first = list ? n0 : 0;
+        end = list ? n : n0;
+        rank = (uint64_t)((b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2)));
+        nwg = gridDim.x / 2;
+    }
+    for (uint64_t idx = first + rank * kHashThreads + threadIdx.x; idx < end; idx += nwg * kHashThreads) {
+        const int2 e = entries[idx];
+        int32_t key = e.x;
+        uint32_t acc = 0;  // wraps like the reference's int accumulator
+        for (int it = 0; it < chain_len; ++it) {
+            int32_t nk;
+            acc += (uint32_t)dep_probe_one(table, mask, key, nk);
+            key = nk;
+        }
+        out[e.y] = (int32_t)(acc ^ (uint32_t)key);
+    }
+}
+
 // Seeded inputs (device): key i = splitmix64(seed, i) (distinct for distinct i),
 // value i = splitmix64(seed ^ 0x5BD1E9955BD1E995, i); query j is a hit for even j
 // (key splitmix64(qseed, j) mod n_keys) and a miss for odd j (key n_keys + j/2, from the
@@ -373,6 +538,57 @@ int xd_dep_probe(const void *table, uint64_t slots, const int32_t *queries, uint
                        static_cast<const int2 *>(table), (uint32_t)(slots - 1), queries, n, chain_len, out, mode,
                        HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()});
     return launch_status("dep_probe_kernel");
+}
+
+size_t xd_dep_route_bytes(uint64_t n) { return route_layout(n).total; }
+
+int xd_dep_route(const void *table, uint64_t slots, const int32_t *queries, uint64_t n, const uint8_t *home_attr,
+                 void *route, size_t route_bytes, void *stream) {
+    XD_REQUIRE(table != nullptr && (reinterpret_cast<uintptr_t>(table) & 7u) == 0, "xd_dep_route: table must be 8-byte aligned");
+    XD_REQUIRE(slots >= 2 && (slots & (slots - 1)) == 0 && slots <= (1ull << 32), "xd_dep_route: slots must be a power of two <= 2^32");
+    XD_REQUIRE(n < (1ull << 31), "xd_dep_route: n must be < 2^31 (int query ids)");
+    XD_REQUIRE(n == 0 || queries != nullptr, "xd_dep_route: NULL queries");
+    const RouteLayout L = route_layout(n);
+    if (route == nullptr || route_bytes < L.total || !aligned16(route))
+        return fail(XD_ERR_WORKSPACE, "xd_dep_route: route buffer missing, misaligned or smaller than xd_dep_route_bytes()");
+    hipStream_t s = (hipStream_t)stream;
+    char *r = static_cast<char *>(route);
+    unsigned long long *header = reinterpret_cast<unsigned long long *>(r);
+    uint32_t *bcnt = reinterpret_cast<uint32_t *>(r + L.bcnt);
+    const uint64_t base = reinterpret_cast<uint64_t>(table);
+    const HomeMap home{home_attr, base / kHomePage, home_mask()};
+    KernelTimer kt("dep_route", s);
+    if (n > 0) {
+        hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)L.nblocks), dim3(kHashThreads), 0, s,
+                           (uint32_t)(slots - 1), queries, n, home, base, bcnt);
+        if (int rc = launch_status("route_count_kernel")) return rc;
+    }
+    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, bcnt, L.nblocks, n, header);
+    if (int rc = launch_status("route_scan_kernel")) return rc;
+    if (n == 0) return XD_OK;
+    hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)L.nblocks), dim3(kHashThreads), 0, s,
+                       (uint32_t)(slots - 1), queries, n, home, base, bcnt, header,
+                       reinterpret_cast<int2 *>(r + L.entries));
+    return launch_status("route_scatter_kernel");
+}
+
+int xd_dep_probe_routed(const void *table, uint64_t slots, const void *route, uint64_t n, int chain_len, int32_t *out,
+                        int mode, void *stream) {
+    XD_REQUIRE(table != nullptr && (reinterpret_cast<uintptr_t>(table) & 7u) == 0, "xd_dep_probe_routed: table must be 8-byte aligned");
+    XD_REQUIRE(slots >= 2 && (slots & (slots - 1)) == 0 && slots <= (1ull << 32), "xd_dep_probe_routed: slots must be a power of two <= 2^32");
+    XD_REQUIRE(n < (1ull << 31), "xd_dep_probe_routed: n must be < 2^31");
+    XD_REQUIRE(route != nullptr && aligned16(route) && (n == 0 || out != nullptr), "xd_dep_probe_routed: NULL route/out");
+    XD_REQUIRE(chain_len >= 1 && chain_len <= 4096, "xd_dep_probe_routed: chain_len must be in [1, 4096]");
+    XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_dep_probe_routed: bad mode");
+    if (n == 0) return XD_OK;
+    const RouteLayout L = route_layout(n);
+    const char *r = static_cast<const char *>(route);
+    KernelTimer kt("dep_probe_routed", (hipStream_t)stream);
+    hipLaunchKernelGGL(dep_probe_routed_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+                       static_cast<const int2 *>(table), (uint32_t)(slots - 1),
+                       reinterpret_cast<const int2 *>(r + L.entries), reinterpret_cast<const unsigned long long *>(r),
+                       chain_len, out, mode);
+    return launch_status("dep_probe_routed_kernel");
 }
 
 int xd_gen_hash_kv(uint64_t *keys, uint64_t *vals, uint64_t n, uint64_t seed, void *stream) {

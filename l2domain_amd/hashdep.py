@@ -58,3 +58,21 @@ class DepTable:
         _lib.call("xd_dep_probe", ptr(self.table), self.slots, ptr(queries) if n else None, n, chain_len,
                   ptr(out) if n else None, mode_id(mode), ptr(self.home_attr), stream_handle(stream))
         return out
+
+    def route(self, queries: torch.Tensor, stream=None) -> torch.Tensor:
+        """The per-die {key, query id} lists of xd_dep_route (the reference's near/far query
+        lists, HASH.cu:244-270), as a device byte buffer for probe_routed()."""
+        n = queries.numel()
+        buf = torch.empty(int(_lib.lib.xd_dep_route_bytes(n)), dtype=torch.uint8, device=queries.device)
+        _lib.call("xd_dep_route", ptr(self.table), self.slots, ptr(queries) if n else None, n, ptr(self.home_attr),
+                  ptr(buf), buf.numel(), stream_handle(stream))
+        return buf
+
+    def probe_routed(self, route: torch.Tensor, n: int, chain_len: int, mode="aware",
+                     out: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+        """probe_dep_sa (HASH.cu:85-116) over pre-routed lists: die d probes list d (aware)."""
+        if out is None:
+            out = torch.empty(n, dtype=torch.int32, device=route.device)
+        _lib.call("xd_dep_probe_routed", ptr(self.table), self.slots, ptr(route), n, chain_len,
+                  ptr(out) if n else None, mode_id(mode), stream_handle(stream))
+        return out

@@ -10,9 +10,13 @@
 // homed on opposite I/O dies and chained into cycles, Q queries of which h percent alternate
 // the hot pools, each following its chain for L dependent probes (xd_dep_*; defaults K =
 // 32000000, Q = 8000000, C = 2^26, L = 4, h = 80, H = 100000, runs = 7 as in :124-130).
-// "Persistent baseline" = XD_MODE_OBLIVIOUS, "Aware" = queries routed on the device to the die
-// that homes their first slot, "Swapped" = to the other die. Correctness as in the reference:
-// the three outputs agree (:345-353); exit 1 otherwise.
+// "Persistent baseline" = XD_MODE_OBLIVIOUS (probe_dep_base), "Aware" / "Swapped" = the routed
+// probe (probe_dep_sa) over the per-die query lists, each die probing its own / the other
+// die's list. As in the reference, the lists are built before the timed runs (the reference
+// builds them on the host, :244-270); here xd_dep_route builds them on the device and its
+// time is reported on its own line (route_ms), with the aware time including it and the
+// single-call XD_MODE_AWARE of xd_dep_probe (routing inside the probe kernel).
+// Correctness as in the reference: the outputs agree (:345-353); exit 1 otherwise.
 //
 // --workload=insert_lookup: the build's insert + lookup configuration on the uint64 table.
 // K keys (xd_gen_hash_kv, seed 42) are inserted into a table of C slots (C a power of
@@ -92,26 +96,43 @@ static int dep_probe(const Options &o) {
            runs);
     printf("table=%.1f MiB chunks=%zu hot_chain_set_per_side=%.1f MiB aware_q0=%lld aware_q1=%lld gpu=%s\n\n",
            tbytes / 1048576.0, tbytes / 8192, H * 8.0 / 1048576.0, nq[0], nq[1], topo.name);
+    const size_t rb = xd_dep_route_bytes((uint64_t)Q);
+    void *route;
+    RUN_HIP(hipMalloc(&route, rb));
+    auto route_ms = [&] { return time_ms(s, [&] { RUN_XD(xd_dep_route(table, C, dq, (uint64_t)Q, home.attr, route, rb, s)); }); };
+    route_ms();
     auto run = [&](int mode) {
-        return time_ms(s, [&] { RUN_XD(xd_dep_probe(table, C, dq, (uint64_t)Q, L, dout[mode], mode, home.attr, s)); });
+        if (mode == 0)
+            return time_ms(s, [&] { RUN_XD(xd_dep_probe(table, C, dq, (uint64_t)Q, L, dout[0], 0, home.attr, s)); });
+        return time_ms(s, [&] { RUN_XD(xd_dep_probe_routed(table, C, route, (uint64_t)Q, L, dout[mode], mode, s)); });
+    };
+    auto run_fly = [&] {
+        return time_ms(s, [&] { RUN_XD(xd_dep_probe(table, C, dq, (uint64_t)Q, L, dout[1], XD_MODE_AWARE, home.attr, s)); });
     };
     for (int mode = 0; mode < 3; ++mode) run(mode);
-    std::vector<int32_t> r0((size_t)Q), r1((size_t)Q), r2((size_t)Q);
+    std::vector<int32_t> r0((size_t)Q), r1((size_t)Q), r2((size_t)Q), r3((size_t)Q);
     RUN_HIP(hipMemcpy(r0.data(), dout[0], (size_t)Q * 4, hipMemcpyDeviceToHost));
     RUN_HIP(hipMemcpy(r1.data(), dout[1], (size_t)Q * 4, hipMemcpyDeviceToHost));
     RUN_HIP(hipMemcpy(r2.data(), dout[2], (size_t)Q * 4, hipMemcpyDeviceToHost));
-    const bool pass = r0 == r1 && r0 == r2;
+    run_fly();
+    RUN_HIP(hipMemcpy(r3.data(), dout[1], (size_t)Q * 4, hipMemcpyDeviceToHost));
+    const bool pass = r0 == r1 && r0 == r2 && r0 == r3;
     printf("Correctness: %s\n\n", pass ? "PASS" : "FAIL");
-    double tbm = 0, ta = 0, ts = 0;
+    double tbm = 0, ta = 0, ts = 0, tr = 0, tf = 0;
     for (int r = 0; r < runs; ++r) {
         tbm += run(0);
         ta += run(1);
         ts += run(2);
+        tr += route_ms();
+        tf += run_fly();
     }
-    const double b = tbm / runs, a = ta / runs, w = ts / runs;
+    const double b = tbm / runs, a = ta / runs, w = ts / runs, rt = tr / runs, fl = tf / runs;
     printf("%-28s %8.3f ms\n", "Persistent baseline", b);
     printf("%-28s %8.3f ms  (speedup %.2fx)\n", "Aware", a, b / a);
     printf("%-28s %8.3f ms  (speedup %.2fx)\n", "Swapped", w, b / w);
+    printf("route_ms=%.6f aware_incl_route_ms=%.6f aware_incl_route_speedup=%.3f aware_single_call_ms=%.6f "
+           "aware_single_call_speedup=%.3f\n",
+           rt, a + rt, b / (a + rt), fl, b / fl);
     printf("mprobes_per_s baseline=%.1f aware=%.1f swapped=%.1f\n", (double)Q * L / (b * 1e3), (double)Q * L / (a * 1e3),
            (double)Q * L / (w * 1e3));
     printf("RESULT baseline_ms=%.6f aware_ms=%.6f swapped_ms=%.6f aware_speedup=%.6f swapped_speedup=%.6f pass=%s\n", b, a,
@@ -122,6 +143,7 @@ static int dep_probe(const Options &o) {
     csv_append(o.csv, "K,Q,C,effective_load,L,h,H,baseline_ms,aware_ms,swapped_ms,aware_speedup,swapped_speedup,pass",
                row);
     for (auto p : dout) (void)hipFree(p);
+    (void)hipFree(route);
     (void)hipFree(dq);
     (void)hipFree(raw);
     return pass ? 0 : 1;

@@ -26,3 +26,34 @@ def test_dep_probe_matches_oracle(K, slots, H, Q, hot, L):
     for mode in MODES:
         got = t.probe(dq, L, mode=mode).cpu().numpy()
         np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("K,slots,H,Q,hot,L", [(1000, 1 << 11, 100, 1, 80, 4), (1000, 1 << 11, 100, 4097, 80, 2),
+                                               (1 << 18, 1 << 20, 10000, 1 << 18, 80, 4),
+                                               (50000, 1 << 16, 20000, 3 * 4096 + 5, 100, 9)])
+def test_routed_probe_matches_oracle(K, slots, H, Q, hot, L):
+    """xd_dep_route + xd_dep_probe_routed: the lists hold every query once, in query order per
+    die, each on the die homing its first slot; the routed probe's outputs equal the oracle's."""
+    t = DepTable(K, slots, H)
+    q = t.queries(Q, hot)
+    want = ora.dep_probe(t.host_table, slots, q, L)
+    dq = torch.from_numpy(q).cuda()
+    route = t.route(dq)
+    torch.cuda.synchronize()
+    raw = route.cpu().numpy()
+    n0, n = int(raw[:8].view(np.uint64)[0]), int(raw[8:16].view(np.uint64)[0])
+    assert n == Q and 0 <= n0 <= Q
+    nblocks = (Q + 4095) // 4096
+    off = (256 + 4 * nblocks + 255) // 256 * 256
+    ent = raw[off: off + 8 * Q].view(np.int32).reshape(Q, 2)
+    attr = t.home_attr.cpu().numpy()
+    base = t.table.data_ptr()
+    die = np.array([(((base + (ora.mix32(int(k)) & (slots - 1)) * 8) >> 13) & 1)
+                    ^ int(attr[((base + (ora.mix32(int(k)) & (slots - 1)) * 8) >> 21) - (base >> 21)]) for k in q])
+    ids0, ids1 = np.nonzero(die == 0)[0], np.nonzero(die == 1)[0]
+    np.testing.assert_array_equal(ent[:n0, 1], ids0)
+    np.testing.assert_array_equal(ent[n0:, 1], ids1)
+    np.testing.assert_array_equal(ent[:, 0], q[ent[:, 1]])
+    for mode in MODES:
+        got = t.probe_routed(route, Q, L, mode=mode).cpu().numpy()
+        np.testing.assert_array_equal(got, want)

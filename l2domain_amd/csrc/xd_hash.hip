@@ -228,13 +228,16 @@ __device__ __forceinline__ int32_t dep_probe_one(const int2 *__restrict__ table,
     bool found = false;
     int32_t nk = key;
     for (uint64_t step = 0; step <= (uint64_t)mask; ++step) {
-        const int2 e = table[slot];
-        if (e.x == key) {
+        // one 8-byte load per entry: fetching the successor separately after a match would
+        // send a second request for the same line
+        const uint64_t e = reinterpret_cast<const uint64_t *>(table)[slot];
+        const int32_t ek = (int32_t)(uint32_t)e;
+        if (ek == key) {
             found = true;
-            nk = e.y;
+            nk = (int32_t)(uint32_t)(e >> 32);
             break;
         }
-        if (e.x == -1) break;
+        if (ek == -1) break;
         slot = (slot + 1) & mask;
     }
     next = nk;

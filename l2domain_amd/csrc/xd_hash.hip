@@ -189,13 +189,17 @@ hash_lookup_kernel(const Slot *__restrict__ table, uint64_t mask, const uint64_t
         uint8_t f = 0;
         if (q != kEmpty) {
             for (uint64_t step = 0; step < max_probe; ++step) {
-                const Slot e = table[s];
-                if (e.key == q) {
-                    v = e.val;
+                // the whole 16-byte slot in one load: reading the value after a key match
+                // would send a second request for the same line
+                const uint4 e = reinterpret_cast<const uint4 *>(table)[s];
+                asm volatile("" ::"v"(e.z), "v"(e.w));  // keeps the value in the same load
+                const uint64_t ek = (uint64_t)e.x | ((uint64_t)e.y << 32);
+                if (ek == q) {
+                    v = (uint64_t)e.z | ((uint64_t)e.w << 32);
                     f = 1;
                     break;
                 }
-                if (e.key == kEmpty) break;
+                if (ek == kEmpty) break;
                 s = (s + 1) & mask;
             }
         }

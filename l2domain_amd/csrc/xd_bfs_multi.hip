@@ -216,23 +216,22 @@ multi_level_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict
             // the claim is a compare-and-swap on the vertex's own level entry (16 vertices per
             // line, where a bitmap word shares its line with 512 and serialises), and all
             // claims of a step are issued before any result is used
-            uint32_t old[kMUnroll];
+            // the work side of a candidate is read together with its claim, not after it
+            uint32_t old[kMUnroll], f[kMUnroll];
 #pragma unroll
             for (int u = 0; u < kMUnroll; ++u) {
                 old[u] = 0u;
-                if (dst[u] >= 0 && !(w[u] & (1ull << (dst[u] & 63))))
+                f[u] = 0u;
+                if (dst[u] >= 0 && !(w[u] & (1ull << (dst[u] & 63)))) {
                     old[u] = atomicCAS(level + dst[u], kMUnv, depth + 1u);
+                    if (routed) f[u] = (uint32_t)(work_side[dst[u]] & 1u);
+                }
             }
             bool take[kMUnroll];
-            uint32_t f[kMUnroll];
 #pragma unroll
             for (int u = 0; u < kMUnroll; ++u) {
                 take[u] = old[u] == kMUnv;
-                f[u] = 0;
-                if (take[u]) {
-                    atomicOr(visited + (dst[u] >> 6), 1ull << (dst[u] & 63));  // filter of later levels; no return
-                    if (routed) f[u] = (uint32_t)(work_side[dst[u]] & 1u);
-                }
+                if (take[u]) atomicOr(visited + (dst[u] >> 6), 1ull << (dst[u] & 63));  // filter of later levels
             }
 #pragma unroll
             for (int u = 0; u < kMUnroll; ++u) st.append(take[u], f[u], dst[u]);

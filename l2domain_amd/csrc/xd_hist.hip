@@ -373,71 +373,77 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     // Each wave walks the tiles t0 + wave, t0 + wave + 16, ...: lane i first fetches the run
     // bounds of 64 of them, then the wave counts run after run. A run is read as 16-byte
     // vectors (8 keys); the first two vectors per lane of the next kRunsAhead runs are in
-    // flight while the current run is counted.
+    // flight while the current run is counted. Every load is issued unconditionally, with its
+    // index clamped into the run (a run never leaves its tile) and the elements outside the
+    // run discarded by count_vec: a load under a branch makes the compiler wait for every
+    // load in flight where the branches join, which would empty the pipeline.
     for (int tb = it.t0 + wave; tb < it.t1; tb += kP2Waves * kWave) {
         const int tl = tb + lane * kP2Waves;
-        uint32_t rs = 0, re = 0;
-        if (tl < it.t1) {
-            const uint32_t *o = offs + (size_t)tl * (nb + 1) + b;
-            rs = o[0];
-            re = o[1];
-        }
+        const bool tok = tl < it.t1;
+        const uint32_t *o = offs + (size_t)(tok ? tl : it.t1 - 1) * (nb + 1) + b;
+        const uint32_t rs0 = o[0], re0 = o[1];
+        const uint32_t rs = tok ? rs0 : 0u, re = tok ? re0 : 0u;
         const int ntl = min(kWave, (it.t1 - tb + kP2Waves - 1) / kP2Waves);
+        // lanes past the end of a run re-read the run's last vector, a line already fetched
         auto load2 = [&](int i, uint4 &v0, uint4 &v1) {
             const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
             const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
             const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
-            const uint32_t v = (s0 >> 3) + (uint32_t)lane, vend = (e0 + 7) >> 3;
-            v0 = v < vend ? run[v] : make_uint4(0, 0, 0, 0);
-            v1 = v + kWave < vend ? run[v + kWave] : make_uint4(0, 0, 0, 0);
+            const uint32_t v = (s0 >> 3) + (uint32_t)lane;
+            const uint32_t last = max((e0 + 7) >> 3, (s0 >> 3) + 1) - 1;  // < kTileVecs
+            v0 = run[min(v, last)];
+            v1 = run[min(v + (uint32_t)kWave, last)];
         };
-        // software pipeline: the runs i + 1 .. i + kRunsAhead are in flight while run i is
-        // counted (ring of register buffers, statically indexed by the unrolled j)
-        uint4 r0[kRunsAhead], r1[kRunsAhead];
-#pragma unroll
-        for (int j = 0; j < kRunsAhead; ++j) {
-            r0[j] = r1[j] = make_uint4(0, 0, 0, 0);
-            if (j < ntl) load2(j, r0[j], r1[j]);
-        }
-        for (int i0 = 0; i0 < ntl; i0 += kRunsAhead) {
-#pragma unroll
-            for (int j = 0; j < kRunsAhead; ++j) {
-                const int i = i0 + j;
-                if (i >= ntl) break;
-                const uint4 c0 = r0[j], c1 = r1[j];
-                if (i + kRunsAhead < ntl) load2(i + kRunsAhead, r0[j], r1[j]);
-                const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
-                const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
-                const uint32_t v = (s0 >> 3) + (uint32_t)lane;
-                // Hot-key vote on the first key of every lane's first vector: keep the current
-                // hot key while a quarter of the samples match it, else adopt the first
-                // sample if a quarter of the samples match that one.
-                const uint32_t e8 = 8 * v;
-                const bool sv = e8 - s0 < e0 - s0;
-                const uint32_t sk = c0.x & 0xffffu;
-                if (__builtin_popcountll(__ballot(sv && sk == hot)) < kWave / 4) {
-                    const uint64_t svm = __ballot(sv);
-                    if (svm) {
-                        const uint32_t cand = (uint32_t)__builtin_amdgcn_readlane((int)sk, __builtin_ctzll(svm));
-                        if (__builtin_popcountll(__ballot(sv && sk == cand)) >= kWave / 4) {
-                            flush_hot();
-                            hot = cand;
-                        }
+        auto count_run = [&](int i, const uint4 &c0, const uint4 &c1) {
+            const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
+            const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
+            const uint32_t v = (s0 >> 3) + (uint32_t)lane;
+            // Hot-key vote on the first key of every lane's first vector: keep the current
+            // hot key while a quarter of the samples match it, else adopt the first sample if
+            // a quarter of the samples match that one.
+            const uint32_t e8 = 8 * v;
+            const bool sv = e8 - s0 < e0 - s0;
+            const uint32_t sk = c0.x & 0xffffu;
+            if (__builtin_popcountll(__ballot(sv && sk == hot)) < kWave / 4) {
+                const uint64_t svm = __ballot(sv);
+                if (svm) {
+                    const uint32_t cand = (uint32_t)__builtin_amdgcn_readlane((int)sk, __builtin_ctzll(svm));
+                    if (__builtin_popcountll(__ballot(sv && sk == cand)) >= kWave / 4) {
+                        flush_hot();
+                        hot = cand;
                     }
                 }
-                count_vec(h, c0, e8, s0, e0, hot, hc);
-                count_vec(h, c1, 8 * (v + kWave), s0, e0, hot, hc);
-                // long runs (the hot bucket): remaining vectors, two per lane per trip
-                const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
-                const uint32_t vend = (e0 + 7) >> 3;
-                for (uint32_t u = v + 2 * kWave; u < vend; u += 2 * kWave) {
-                    const uint4 a0 = run[u];
-                    const uint4 a1 = u + kWave < vend ? run[u + kWave] : make_uint4(0, 0, 0, 0);
-                    count_vec(h, a0, 8 * u, s0, e0, hot, hc);
-                    count_vec(h, a1, 8 * (u + kWave), s0, e0, hot, hc);
-                }
+            }
+            count_vec(h, c0, e8, s0, e0, hot, hc);
+            count_vec(h, c1, 8 * (v + kWave), s0, e0, hot, hc);
+            // long runs (the hot bucket): the remaining vectors, two per lane per trip, in a
+            // loop whose trip count is the same for every lane
+            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
+            const uint32_t vend = (e0 + 7) >> 3;
+            for (uint32_t u0 = (s0 >> 3) + 2 * kWave; u0 < vend; u0 += 2 * kWave) {
+                const uint32_t u = u0 + (uint32_t)lane;
+                const uint4 a0 = run[min(u, vend - 1)];
+                const uint4 a1 = run[min(u + (uint32_t)kWave, vend - 1)];
+                count_vec(h, a0, 8 * u, s0, e0, hot, hc);
+                count_vec(h, a1, 8 * (u + kWave), s0, e0, hot, hc);
+            }
+        };
+        // software pipeline over a ring of register buffers, statically indexed
+        uint4 r0[kRunsAhead], r1[kRunsAhead];
+#pragma unroll
+        for (int j = 0; j < kRunsAhead; ++j) load2(min(j, ntl - 1), r0[j], r1[j]);
+        int i0 = 0;
+        for (; i0 + kRunsAhead <= ntl; i0 += kRunsAhead) {
+#pragma unroll
+            for (int j = 0; j < kRunsAhead; ++j) {
+                const uint4 c0 = r0[j], c1 = r1[j];
+                load2(min(i0 + j + kRunsAhead, ntl - 1), r0[j], r1[j]);
+                count_run(i0 + j, c0, c1);
             }
         }
+#pragma unroll
+        for (int j = 0; j < kRunsAhead; ++j)
+            if (i0 + j < ntl) count_run(i0 + j, r0[j], r1[j]);
     }
     if (hot < kTrash) flush_hot();
     __syncthreads();

@@ -175,17 +175,19 @@ class Hist:
     def __init__(self, n=1 << 28, num_bins=1 << 20):
         import torch
         from l2domain_amd import gen
+        from l2domain_amd.domain import home_map
         from l2domain_amd.histogram import HIST_SEED, ZIPF_S, Histogram
         self.n, self.num_bins = n, num_bins
         self.keys = gen.zipf_keys_device(n, num_bins, HIST_SEED, ZIPF_S)
+        self.home = home_map(self.keys.view(torch.uint8))  # the aware mode reads near chunks
         self.h = Histogram(n, num_bins)
         self.counts = torch.empty(num_bins, dtype=torch.int32, device="cuda")
         torch.cuda.synchronize()
-        # 4 B per key read + 4 B per counter written
+        # algorithmic bytes: 4 B per key read + 4 B per counter written
         self.bytes = 4 * n + 4 * num_bins
 
     def step(self, mode):
-        self.h(self.keys, self.counts, mode=mode)
+        self.h(self.keys, self.counts, mode=mode, home_attr=self.home)
 
     def throughput(self, sec_per_step):
         return self.n / sec_per_step / 1e9
@@ -206,9 +208,10 @@ class Hist:
     def roofline(self, sec_per_launch):
         # dominant kernel: the partition pass; its algorithmic traffic is the 4 B/key read.
         # traffic: rocprofv3 --pmc FETCH_SIZE (x2.000, copy-kernel calibration) + WRITE_SIZE of
-        # this kernel at this configuration: 1,073,846,600 B read + 541,589,504 B written.
+        # the aware (routed) launch at this configuration: 1,073,954,202 B read + 540,019,405 B
+        # written.
         achieved = 4 * self.n / sec_per_launch / 1e9
-        traffic = 1615436104 if (self.n, self.num_bins) == (1 << 28, 1 << 20) else None
+        traffic = 1613973607 if (self.n, self.num_bins) == (1 << 28, 1 << 20) else None
         return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "hist_partition_kernel",
                 "algorithmic_bytes_per_launch": 4 * self.n}
@@ -284,7 +287,7 @@ class Hash:
         return ok
 
     def roofline(self, sec_per_launch):
-        # lookup = 8 B key + 16 B slot + 8 B value + 1 B found per query
+        # algorithmic bytes: lookup = 8 B key + 16 B slot + 8 B value + 1 B found per query
         achieved = 33 * self.n / sec_per_launch / 1e9
         return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "hash_lookup_kernel",

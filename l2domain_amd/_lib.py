@@ -86,7 +86,7 @@ SIGNATURES: dict[str, tuple] = {
     "xd_gemv_f32": (I, [VP, VP, VP, I, I, I, VP, VP, SZ, VP]),
     "xd_gemv_f16f32": (I, [VP, VP, VP, I, I, I, VP, VP, SZ, VP]),
     "xd_hist_workspace_size": (SZ, [SZ, U32]),
-    "xd_hist_u32": (I, [VP, SZ, VP, U32, I, VP, SZ, VP]),
+    "xd_hist_u32": (I, [VP, SZ, VP, U32, I, VP, VP, SZ, VP]),
     "xd_hist256_workspace_size": (SZ, []),
     "xd_hist256_u32bytes": (I, [VP, SZ, VP, I, VP, VP, SZ, VP]),
     "xd_hash_table_bytes": (SZ, [U64]),

@@ -21,7 +21,9 @@ ZIPF_S = 1.1
 
 
 class Histogram:
-    """Owns the workspace of xd_hist_u32 for inputs of up to `max_keys` keys."""
+    """Owns the workspace of xd_hist_u32 for inputs of up to `max_keys` keys. `home_attr` is
+    the xd_home_map of the keys buffer the aware and rotated modes route by (None: the
+    address-mask prediction)."""
 
     def __init__(self, max_keys: int, num_bins: int, device: int | str = 0):
         self.num_bins = int(num_bins)
@@ -34,7 +36,7 @@ class Histogram:
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
 
     def __call__(self, keys: torch.Tensor, counts: torch.Tensor | None = None, mode="aware",
-                 stream: torch.cuda.Stream | None = None) -> torch.Tensor:
+                 home_attr: torch.Tensor | None = None, stream: torch.cuda.Stream | None = None) -> torch.Tensor:
         if keys.dtype not in (torch.int32, torch.uint32) or keys.dim() != 1:
             raise TypeError("keys must be a 1-D 32-bit integer tensor")
         n = keys.numel()
@@ -45,7 +47,7 @@ class Histogram:
         if counts.numel() != self.num_bins or counts.element_size() != 4:
             raise ValueError("counts must hold num_bins 32-bit counters")
         _lib.call("xd_hist_u32", ptr(keys) if n else None, n, ptr(counts), self.num_bins, mode_id(mode),
-                  ptr(self.workspace), self.workspace.numel(), stream_handle(stream))
+                  ptr(home_attr), ptr(self.workspace), self.workspace.numel(), stream_handle(stream))
         return counts
 
 

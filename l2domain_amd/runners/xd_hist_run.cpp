@@ -149,6 +149,7 @@ static int run_zipf(const Options &o) {
     RUN_HIP(hipMalloc(&counts, (size_t)bins * 4));
     RUN_HIP(hipMemcpy(dthr, thr.data(), (size_t)bins * 8, hipMemcpyHostToDevice));
     RUN_XD(xd_gen_zipf_keys(keys, n, dthr, bins, seed, 1, s));
+    HomeMap home(keys, n * 4, s);  // the aware mode reads the key chunks each die homes
     const size_t wsb = xd_hist_workspace_size(n, bins);
     void *ws = nullptr;
     RUN_HIP(hipMalloc(&ws, wsb));
@@ -166,17 +167,17 @@ static int run_zipf(const Options &o) {
     bool ok[3];
     for (int mode = 0; mode < 3; ++mode) {
         RUN_HIP(hipMemset(counts, 0xff, (size_t)bins * 4));
-        RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, ws, wsb, s));
+        RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, home.attr, ws, wsb, s));
         RUN_HIP(hipMemcpy(got.data(), counts, (size_t)bins * 4, hipMemcpyDeviceToHost));
         ok[mode] = got == ref;
     }
     for (int mode = 0; mode < 3; ++mode)
-        for (int w = 0; w < 3; ++w) RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, ws, wsb, s));
+        for (int w = 0; w < 3; ++w) RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, home.attr, ws, wsb, s));
     double ms[3] = {0, 0, 0};
     for (int r = 0; r < runs; ++r)
         for (int mode = 0; mode < 3; ++mode) {
             if (!cache_mode) flush(s);
-            ms[mode] += time_ms(s, [&] { RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, ws, wsb, s)); });
+            ms[mode] += time_ms(s, [&] { RUN_XD(xd_hist_u32(keys, n, counts, bins, mode, home.attr, ws, wsb, s)); });
         }
     for (double &m : ms) m /= runs;
     const char *P[2] = {"FAIL", "PASS"};

@@ -28,7 +28,7 @@ def test_splitmix64_is_a_stream_of_the_seed():
 
 
 def test_mix32_known_answers():
-    # lowbias32 finaliser of GEMV.cu:56-63; values computed independently (SURVEY 8(a) KATs).
+    # lowbias32 finaliser of GEMV.cu:56-63; known-answer values computed independently.
     kat = {0: 0, 1: 0x688990C0, 2: 0xD1132181, 4242: 0xE0D78B3B, 0xFFFFFFFF: 0x6768824A}
     for k, v in kat.items():
         assert ora.mix32(k) == v

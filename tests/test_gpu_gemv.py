@@ -44,7 +44,7 @@ def run(A: np.ndarray, x: np.ndarray, mode, mapped: bool = False, ws=None) -> np
     if ws is not None:
         S = A.shape[1] * A.itemsize // 8192
         words = 8 * A.shape[0] if S == 2 else 4 * A.shape[0]  # S == 2: one 64-bit word per row
-        assert int(torch.count_nonzero(ws[:words])) == 0, "row words / counters not left at zero"
+        assert int(torch.count_nonzero(ws[:words])) == 0, "row words / counters / pieces not left at zero"
     return y.cpu().numpy()
 
 
@@ -193,6 +193,26 @@ def test_split_row_home_ragged(M, K):
         y = run(A, x, mode, mapped=True)
         assert rel_err(y, ref) <= 1e-3
         assert np.all(np.abs(y - ref) <= 1e-3 * yabs + 1e-30)
+
+
+@pytest.mark.parametrize("dtype,M,K", [("f32", 2, 3072), ("f32", 100, 7168), ("f16", 6, 6144), ("f16", 34, 14336),
+                                         ("f16", 7, 14336)])
+def test_half_chunk_home_ragged(dtype, M, K):
+    # rows of an odd number of 4 KiB halves (H = 3 or 7): 8 KiB chunks routed by home, a chunk
+    # straddling two rows feeds both; odd M takes the oblivious kernel instead
+    if dtype == "f32":
+        A, x = gen.gemv_f32_inputs(M, K, seed=M * 5 + K)
+        tol = 1e-3
+    else:
+        A, x = gen.gemv_f16_inputs(M, K, w_seed=M * 5 + K, x_seed=M * 7 + K)
+        tol = 2e-2
+    ref, yabs = ora.gemv_f64(A, x)
+    assert (workspace(M, K, torch.float32 if dtype == "f32" else torch.float16) is None) == (M % 2 == 1)
+    for mode in MODES:
+        y = run(A, x, mode, mapped=True)
+        assert np.all(np.isfinite(y))
+        assert rel_err(y, ref) <= tol
+        assert np.all(np.abs(y - ref) <= tol * yabs + 1e-30)
 
 
 def test_split_row_without_workspace_falls_back():

@@ -31,8 +31,10 @@
 
 namespace xd {
 
+// 32768 counters = 128 KB of LDS per counting workgroup (16384-bin buckets, two workgroups
+// per CU, counted no faster: 188 against 186 us at 2^28 keys, with a slower plan and merge).
 constexpr int kHB = 15;
-constexpr uint32_t kBucketBins = 1u << kHB;  // 32768 counters = 128 KB of LDS
+constexpr uint32_t kBucketBins = 1u << kHB;
 // Keys per partition tile: whole 16-byte vectors per thread and whole 16 KiB pairs per
 // routed tile. Longer tiles give the count pass longer runs (32768: count 176 us at 2^28
 // keys against 208 us at 16384); 24576 measured fastest for the XCD-aware call.
@@ -130,13 +132,15 @@ struct PartSrc {
 };
 
 // PACK (at most kPackBuckets buckets, full and routed kinds): each counter column takes one
-// lane of each of the 16 waves, so a key's slot inside its column is below 16 * 32 = 512 and
-// shares the key's register (key or the spare 2^20 in bits 0-20, slot in bits 21-29): the
-// live state across the scan is then one register per key.
+// lane of each of the 16 waves, so a key's slot inside its column is below 16 * (keys per
+// thread) and shares the key's register (key or the spare 2^20 in bits 0-20, slot from bit
+// 21): the live state across the scan is then one register per key.
 constexpr int kPackBuckets = kColCounters / kWave;
 constexpr uint32_t kPackSpare = (uint32_t)kPackBuckets << kHB;
 constexpr int kPackShift = 21;
-static_assert(kP1Threads / kWave * 4 * kP1Vec <= (1 << (32 - kPackShift)), "packed slots overflow");
+static_assert(kPackSpare == (1u << (kPackShift - 1)), "packed keys and the spare fit below the slot bits");
+static_assert(kP1Threads / kWave * 4 * kP1Vec * (kWave * kPackBuckets / kColCounters) <= (1 << (32 - kPackShift)),
+              "packed slots overflow");
 
 template <int KIND, bool PACK>
 __global__ void __launch_bounds__(kP1Threads)
@@ -424,10 +428,6 @@ hist_plan_kernel(const uint32_t *__restrict__ tot, int nb, int ntiles, int per_x
 // 3. count
 // ---------------------------------------------------------------------------------------
 constexpr uint32_t kTrash = kBucketBins;  // LDS slot that absorbs elements outside a run
-#ifndef XD_HIST_RUNS_AHEAD
-#define XD_HIST_RUNS_AHEAD 2
-#endif
-constexpr int kRunsAhead = XD_HIST_RUNS_AHEAD;  // runs loaded ahead of the one being counted
 
 // Counts the 8 u16 keys of one 16-byte vector whose first element has index `e`, for the
 // run [s0, e0). Keys equal to the wave's current hot key go to the per-lane register
@@ -475,40 +475,67 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
         if (lane == 0 && tot_hot) atomicAdd(&h[hot], tot_hot);
         hc = 0;
     };
-    // Each wave walks the tiles t0 + wave, t0 + wave + 16, ...: lane i first fetches the run
-    // bounds of 64 of them, then the wave counts run after run. A run is read as 16-byte
-    // vectors (8 keys); the first two vectors per lane of the next kRunsAhead runs are in
-    // flight while the current run is counted. Every load is issued unconditionally, with its
-    // index clamped into the run (a run never leaves its tile) and the elements outside the
-    // run discarded by count_vec: a load under a branch makes the compiler wait for every
-    // load in flight where the branches join, which would empty the pipeline.
+    // Each wave walks the tiles t0 + wave, t0 + wave + 16, ...: lane i fetches the bounds of
+    // the bucket's run in 64 of them, and the wave counts the concatenation of those runs as
+    // a stream of 16-byte vectors (8 keys), vector G + lane on lane `lane`, so every lane has
+    // a vector whatever the run lengths. A run's vectors start at the exclusive prefix of the
+    // vector counts; the runs holding vectors [G, G + 64) form a short window found with two
+    // ballots, and a uniform walk over it gives each lane its run. The next 128 vectors are
+    // loaded while the current 128 are counted. Every load is issued unconditionally (past
+    // the stream a lane re-reads the last vector and counts nothing): a load under a branch
+    // makes the compiler wait for every load in flight where the branches join.
     for (int tb = it.t0 + wave; tb < it.t1; tb += kP2Waves * kWave) {
         const int tl = tb + lane * kP2Waves;
         const bool tok = tl < it.t1;
         const uint32_t *o = offs + (size_t)(tok ? tl : it.t1 - 1) * (nb + 1) + b;
         const uint32_t rs0 = o[0], re0 = o[1];
         const uint32_t rs = tok ? rs0 : 0u, re = tok ? re0 : 0u;
-        const int ntl = min(kWave, (it.t1 - tb + kP2Waves - 1) / kP2Waves);
-        // lanes past the end of a run re-read the run's last vector, a line already fetched
-        auto load2 = [&](int i, uint4 &v0, uint4 &v1) {
-            const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
-            const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
-            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
-            const uint32_t v = (s0 >> 3) + (uint32_t)lane;
-            const uint32_t last = max((e0 + 7) >> 3, (s0 >> 3) + 1) - 1;  // < kTileVecs
-            v0 = run[min(v, last)];
-            v1 = run[min(v + (uint32_t)kWave, last)];
+        const uint32_t nvec = re > rs ? ((re + 7) >> 3) - (rs >> 3) : 0u;
+        const uint32_t incl = wave_incl_scan_u32(nvec);
+        const uint32_t excl = incl - nvec;
+        const uint32_t T = (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+        if (T == 0) continue;
+        // vector G + lane of the stream: q, the key index of its first element in its tile (e8;
+        // past the stream: the run's end, so nothing is counted) and its run's bounds
+        auto fetch = [&](uint32_t G, uint4 &q, uint32_t &e8, uint32_t &s0, uint32_t &e0) {
+            const uint32_t g = G + (uint32_t)lane;
+            const uint32_t gc = min(g, T - 1);
+            const uint32_t Gq = min(G, T - 1), Gz = min(G + (uint32_t)kWave - 1, T - 1);
+            const int jlo = __builtin_ctzll(__ballot(incl > Gq));
+            const int jhi = __builtin_ctzll(__ballot(incl > Gz));
+            int jj = jlo;
+            uint32_t ex = 0, ss = 0, ee = 0;
+            for (int jr = jlo; jr <= jhi; ++jr) {
+                const uint32_t exj = (uint32_t)__builtin_amdgcn_readlane((int)excl, jr);
+                const uint32_t rsj = (uint32_t)__builtin_amdgcn_readlane((int)rs, jr);
+                const uint32_t rej = (uint32_t)__builtin_amdgcn_readlane((int)re, jr);
+                const bool in = gc >= exj;  // the last such run holds the vector (empty runs share
+                jj = in ? jr : jj;          // their successor's start and lose to it)
+                ex = in ? exj : ex;
+                ss = in ? rsj : ss;
+                ee = in ? rej : ee;
+            }
+            const uint32_t v = (ss >> 3) + (gc - ex);
+            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + jj * kP2Waves) * kTileKeys);
+            q = run[v];
+            e8 = g < T ? 8 * v : ee;
+            s0 = ss;
+            e0 = ee;
         };
-        auto count_run = [&](int i, const uint4 &c0, const uint4 &c1) {
-            const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)rs, i);
-            const uint32_t e0 = (uint32_t)__builtin_amdgcn_readlane((int)re, i);
-            const uint32_t v = (s0 >> 3) + (uint32_t)lane;
+        uint4 qa, qb;
+        uint32_t ea, eb, sa, sb, xa, xb;
+        fetch(0, qa, ea, sa, xa);
+        fetch(kWave, qb, eb, sb, xb);
+        for (uint32_t G = 0; G < T; G += 2 * kWave) {
+            uint4 na, nb2;
+            uint32_t fa, fb, ta, tb2, ya, yb;
+            fetch(G + 2 * kWave, na, fa, ta, ya);
+            fetch(G + 3 * kWave, nb2, fb, tb2, yb);
             // Hot-key vote on the first key of every lane's first vector: keep the current
             // hot key while a quarter of the samples match it, else adopt the first sample if
             // a quarter of the samples match that one.
-            const uint32_t e8 = 8 * v;
-            const bool sv = e8 - s0 < e0 - s0;
-            const uint32_t sk = c0.x & 0xffffu;
+            const bool sv = ea - sa < xa - sa;
+            const uint32_t sk = qa.x & 0xffffu;
             if (__builtin_popcountll(__ballot(sv && sk == hot)) < kWave / 4) {
                 const uint64_t svm = __ballot(sv);
                 if (svm) {
@@ -519,36 +546,17 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
                     }
                 }
             }
-            count_vec(h, c0, e8, s0, e0, hot, hc);
-            count_vec(h, c1, 8 * (v + kWave), s0, e0, hot, hc);
-            // long runs (the hot bucket): the remaining vectors, two per lane per trip, in a
-            // loop whose trip count is the same for every lane
-            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + i * kP2Waves) * kTileKeys);
-            const uint32_t vend = (e0 + 7) >> 3;
-            for (uint32_t u0 = (s0 >> 3) + 2 * kWave; u0 < vend; u0 += 2 * kWave) {
-                const uint32_t u = u0 + (uint32_t)lane;
-                const uint4 a0 = run[min(u, vend - 1)];
-                const uint4 a1 = run[min(u + (uint32_t)kWave, vend - 1)];
-                count_vec(h, a0, 8 * u, s0, e0, hot, hc);
-                count_vec(h, a1, 8 * (u + kWave), s0, e0, hot, hc);
-            }
-        };
-        // software pipeline over a ring of register buffers, statically indexed
-        uint4 r0[kRunsAhead], r1[kRunsAhead];
-#pragma unroll
-        for (int j = 0; j < kRunsAhead; ++j) load2(min(j, ntl - 1), r0[j], r1[j]);
-        int i0 = 0;
-        for (; i0 + kRunsAhead <= ntl; i0 += kRunsAhead) {
-#pragma unroll
-            for (int j = 0; j < kRunsAhead; ++j) {
-                const uint4 c0 = r0[j], c1 = r1[j];
-                load2(min(i0 + j + kRunsAhead, ntl - 1), r0[j], r1[j]);
-                count_run(i0 + j, c0, c1);
-            }
+            count_vec(h, qa, ea, sa, xa, hot, hc);
+            count_vec(h, qb, eb, sb, xb, hot, hc);
+            qa = na;
+            qb = nb2;
+            ea = fa;
+            eb = fb;
+            sa = ta;
+            sb = tb2;
+            xa = ya;
+            xb = yb;
         }
-#pragma unroll
-        for (int j = 0; j < kRunsAhead; ++j)
-            if (i0 + j < ntl) count_run(i0 + j, r0[j], r1[j]);
     }
     if (hot < kTrash) flush_hot();
     __syncthreads();

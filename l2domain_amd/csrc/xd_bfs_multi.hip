@@ -215,22 +215,30 @@ multi_level_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict
             for (int u = 0; u < kMUnroll; ++u) w[u] = dst[u] >= 0 ? visited[dst[u] >> 6] : ~0ull;
             // the claim is a compare-and-swap on the vertex's own level entry (16 vertices per
             // line, where a bitmap word shares its line with 512 and serialises), and all
-            // claims of a step are issued before any result is used
-            // the work side of a candidate is read together with its claim, not after it
+            // claims of a step are issued before any result is used. A claim's result is left
+            // undefined on the path that skips it and read only where it was issued: a value
+            // merged at a branch join with a constant makes the compiler wait for the atomic
+            // right there, which put the 8 claims of a step one after another. The work side
+            // is read with the claim, in the home modes, and likewise left undefined elsewhere.
+            // All filters are decided before the first claim is issued: once a conditional
+            // atomic is in flight the compiler cannot count what is outstanding, and it would
+            // wait for everything (the claim included) before testing the next bitmap word.
+            bool pass[kMUnroll];
             uint32_t old[kMUnroll], f[kMUnroll];
 #pragma unroll
-            for (int u = 0; u < kMUnroll; ++u) {
-                old[u] = 0u;
-                f[u] = 0u;
-                if (dst[u] >= 0 && !(w[u] & (1ull << (dst[u] & 63)))) {
+            for (int u = 0; u < kMUnroll; ++u) pass[u] = dst[u] >= 0 && !(w[u] & (1ull << (dst[u] & 63)));
+            uint32_t fw[kMUnroll];
+#pragma unroll
+            for (int u = 0; u < kMUnroll; ++u)
+                if (pass[u]) {
                     old[u] = atomicCAS(level + dst[u], kMUnv, depth + 1u);
-                    if (routed) f[u] = (uint32_t)(work_side[dst[u]] & 1u);
+                    if (routed) fw[u] = work_side[dst[u]];
                 }
-            }
             bool take[kMUnroll];
 #pragma unroll
             for (int u = 0; u < kMUnroll; ++u) {
-                take[u] = old[u] == kMUnv;
+                take[u] = pass[u] && old[u] == kMUnv;
+                f[u] = (routed && take[u]) ? (fw[u] & 1u) : 0u;
                 if (take[u]) atomicOr(visited + (dst[u] >> 6), 1ull << (dst[u] & 63));  // filter of later levels
             }
 #pragma unroll

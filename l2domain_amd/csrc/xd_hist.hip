@@ -7,18 +7,19 @@
 //   merge_histogram256_kernel (136-157): sum of the per-block partials.
 //
 // MI355X design. 2^20 u32 counters (4 MiB) do not fit the 160 KB LDS of a CU, and global
-// atomics on gfx950 run at a fixed ~27 Gatom/s chip-wide (~88 M/s on one hot address)
-// wherever the line lives, so every key must be counted in LDS:
+// atomics on gfx950 run at about 27 Gatom/s chip-wide (about 88 M/s on one hot address),
+// so every key must be counted in LDS:
 //   1. partition: each workgroup multi-splits a tile of kTileKeys keys into 32768-bin buckets
 //      (bucket = key >> 15) and writes the 15-bit in-bucket offsets, grouped by bucket,
 //      as u16 (tile-major), plus the tile's bucket offsets and bucket totals. XCD-aware
 //      mode reads the keys as routed tiles: each I/O die's workgroups read only the 8 KiB
 //      key chunks that die homes (the reference's side-aware chunks); rotated reads the far
 //      chunks; oblivious reads contiguous tiles;
-//   2. plan: deals the counting work items (bucket, tile range) to the buckets in
-//      proportion to their totals; XCD-aware mode lays the items out so that every XCD
-//      gets a contiguous range of buckets (bins range-partitioned per XCD) and an equal
-//      share of keys, and only that XCD's workgroups count them;
+//   2. plan (at the start of every count workgroup, from the per-XCD bucket totals): deals
+//      the counting work items (bucket, tile range) to the buckets in proportion to their
+//      totals; XCD-aware mode lays the items out so that every XCD gets a contiguous range
+//      of buckets (bins range-partitioned per XCD) and an equal share of keys, and only that
+//      XCD's workgroups count them;
 //   3. count: one workgroup per item keeps a 128 KB LDS histogram of its bucket, adds each
 //      key with a ds_add (the wave's most common key is peeled into one add), and writes
 //      the LDS histogram to its partial slot;
@@ -48,15 +49,8 @@ constexpr int kP2Waves = kP2Threads / kWave;
 constexpr int kMergeThreads = 256;
 constexpr int kMergeBins = 1024;  // bins per merge unit (4 per thread)
 constexpr int kMergeUnitsPerBucket = kBucketBins / kMergeBins;
-constexpr int kPlanThreads = kMaxBuckets;
 constexpr uint32_t kSpareKey = (uint32_t)kMaxBuckets << kHB;  // above every valid key (num_bins <= 2^24)
 constexpr uint32_t kColCounters = 2048;  // partition counters per tile (buckets x columns)
-
-struct HistItem {
-    int bucket;  // -1: idle slot
-    int t0, t1;  // tile range
-    int pad;
-};
 
 struct HistBucket {
     int first;  // first item (= partial slot) of this bucket
@@ -65,7 +59,7 @@ struct HistBucket {
 
 struct HistLayout {
     int nb, ntiles, per_xcd, nitems;
-    size_t part, offs, tot, items, buckets, xcdr, partials, total;
+    size_t part, offs, tot, buckets, xcdr, partials, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -86,8 +80,6 @@ static HistLayout hist_layout(size_t n, uint32_t num_bins) {
     size_t o = 0;
     L.tot = o;
     o = align256(o + (size_t)kNumXcd * L.nb * sizeof(uint32_t));
-    L.items = o;
-    o = align256(o + (size_t)L.nitems * sizeof(HistItem));
     L.buckets = o;
     o = align256(o + (size_t)L.nb * sizeof(HistBucket));
     L.xcdr = o;
@@ -330,8 +322,9 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
 }
 
 // ---------------------------------------------------------------------------------------
-// 2. plan (one workgroup; one thread per bucket)
+// 2. plan (run by every count workgroup: one thread per bucket)
 // ---------------------------------------------------------------------------------------
+template <int THREADS>
 __device__ uint32_t block_excl_scan(uint32_t v, uint32_t *wsum, uint32_t *total) {
     const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     const uint32_t incl = wave_incl_scan_u32(v);
@@ -339,7 +332,7 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t *wsum, uint32_t *total)
     __syncthreads();
     if (tid == 0) {
         uint32_t c = 0;
-        for (int w = 0; w < kPlanThreads / kWave; ++w) {
+        for (int w = 0; w < THREADS / kWave; ++w) {
             uint32_t s = wsum[w];
             wsum[w] = c;
             c += s;
@@ -352,76 +345,33 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t *wsum, uint32_t *total)
     return r;
 }
 
-__global__ void __launch_bounds__(kPlanThreads)
-hist_plan_kernel(const uint32_t *__restrict__ tot, int nb, int ntiles, int per_xcd, int mode, HistItem *items,
-                 HistBucket *buckets, int *xcd_range) {
-    __shared__ uint32_t wsum[kPlanThreads / kWave];
-    __shared__ uint32_t s_total, s_nnz_total;
-    __shared__ uint32_t xfirst[kNumXcd];
-    const int b = (int)threadIdx.x;
-    const int nitems = per_xcd * kNumXcd;
-    for (int i = b; i < nitems; i += kPlanThreads) items[i] = HistItem{-1, 0, 0, 0};
-    if (b < kNumXcd) xfirst[b] = 0xffffffffu;
+struct Deal {
+    uint32_t first, count;  // item slots [first, first + count) of the calling thread's bucket
+};
 
+// Thread b < nb gets bucket b's item slots (every thread of the block must call it). The slots
+// are dealt to the buckets in bucket order, in proportion to their keys: bucket b starts at
+// slot nzpre + floor(pre * R / N), R = slots beyond one per non-empty bucket, and the slots
+// end exactly at nitems (the clamps only guard the table).
+template <int THREADS>
+__device__ Deal deal_items(const uint32_t *__restrict__ tot, int nb, int nitems, uint32_t *wsum) {
+    __shared__ uint32_t s_total, s_nnz;
+    const int b = (int)threadIdx.x;
     uint32_t T = 0;
     if (b < nb)
         for (int x = 0; x < kNumXcd; ++x) T += tot[(size_t)x * nb + b];
     const uint32_t nz = (b < nb && T > 0) ? 1u : 0u;
-    const uint32_t pre = block_excl_scan(T, wsum, &s_total);
+    const uint32_t pre = block_excl_scan<THREADS>(T, wsum, &s_total);
     const uint32_t N = s_total;
-    const uint32_t nzpre = block_excl_scan(nz, wsum, &s_nnz_total);
-    const uint32_t nnz = s_nnz_total;
-
-    // The item slots are dealt to the buckets in bucket order, in proportion to their keys:
-    // bucket b starts at slot nzpre + floor(pre * R / N), R = slots beyond one per non-empty
-    // bucket, and the slots end exactly at nitems (the clamps only guard the table).
+    const uint32_t nzpre = block_excl_scan<THREADS>(nz, wsum, &s_nnz);
+    const uint32_t nnz = s_nnz;
     const unsigned long long R = (unsigned long long)nitems - min(nnz, (uint32_t)nitems);
     const uint32_t Nd = N ? N : 1u;
     uint32_t first = nzpre + (uint32_t)(((unsigned long long)pre * R) / Nd);
     uint32_t J = nz ? 1u + (uint32_t)(((unsigned long long)(pre + T) * R) / Nd - ((unsigned long long)pre * R) / Nd) : 0u;
     if (first > (uint32_t)nitems) first = (uint32_t)nitems;
     if (J > (uint32_t)nitems - first) J = (uint32_t)nitems - first;
-
-    if (mode == XD_MODE_OBLIVIOUS) {
-        // One flat list: item g runs on workgroup g.
-        if (b < nb) {
-            buckets[b] = HistBucket{(int)first, (int)J};
-            for (uint32_t j = 0; j < J; ++j)
-                items[first + j] = HistItem{b, (int)((unsigned long long)j * ntiles / J),
-                                            (int)((unsigned long long)(j + 1) * ntiles / J), 0};
-        }
-        if (b < kNumXcd) {  // merge ranges: equal bucket counts
-            xcd_range[2 * b] = (int)((long long)b * nb / kNumXcd);
-            xcd_range[2 * b + 1] = (int)((long long)(b + 1) * nb / kNumXcd);
-        }
-        return;
-    }
-
-    // XCD-aware: slot x * per_xcd + r runs on XCD x, so every XCD counts an equal share of
-    // the keys and almost every bucket lies inside one XCD's slots; the merge pass merges a
-    // bucket on the XCD of its first slot.
-    int x = min((int)(first / (uint32_t)per_xcd), kNumXcd - 1);
-    if (b < nb) {
-        buckets[b] = HistBucket{(int)first, (int)J};
-        for (uint32_t j = 0; j < J; ++j)
-            items[first + j] = HistItem{b, (int)((unsigned long long)j * ntiles / J),
-                                        (int)((unsigned long long)(j + 1) * ntiles / J), 0};
-        atomicMin(&xfirst[x], (uint32_t)b);
-    }
-    __syncthreads();
-    if (b < kNumXcd) {
-        // Ranges: [first bucket of XCD b, first bucket of the next non-empty XCD).
-        int b0 = (xfirst[b] == 0xffffffffu) ? nb : (int)xfirst[b];
-        int b1 = nb;
-        for (int y = b + 1; y < kNumXcd; ++y)
-            if (xfirst[y] != 0xffffffffu) {
-                b1 = (int)xfirst[y];
-                break;
-            }
-        if (b0 > b1) b0 = b1;
-        xcd_range[2 * b] = b0;
-        xcd_range[2 * b + 1] = b1;
-    }
+    return Deal{first, J};
 }
 
 // ---------------------------------------------------------------------------------------
@@ -448,26 +398,64 @@ __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t 
 }
 
 __global__ void __launch_bounds__(kP2Threads)
-hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb,
-                  const HistItem *__restrict__ items, int per_xcd, uint32_t *__restrict__ partials, int mode,
-                  unsigned rot) {
+hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb, int ntiles,
+                  const uint32_t *__restrict__ tot, int per_xcd, uint32_t *__restrict__ partials,
+                  HistBucket *__restrict__ buckets, int *__restrict__ xcd_range, int mode, unsigned rot) {
     __shared__ __attribute__((aligned(16))) uint32_t h[kBucketBins + 4];
+    __shared__ uint32_t wsum[kP2Waves];
+    __shared__ int s_item[3];  // bucket (-1: idle slot), t0, t1
+    __shared__ uint32_t xfirst[kNumXcd];
     const int g = (int)blockIdx.x;
-    int item;
+    const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    int slot;
     if (mode == XD_MODE_OBLIVIOUS) {
-        item = g;
+        slot = g;
     } else {
         XcdSlot s = xcd_slot(g, (int)gridDim.x, mode, rot);
-        item = s.slice * per_xcd + s.rank;
+        slot = s.slice * per_xcd + s.rank;
     }
-    const HistItem it = items[item];
-    if (it.bucket < 0) return;
-    const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+    if (tid == 0) s_item[0] = -1;
+    if (tid < kNumXcd) xfirst[tid] = 0xffffffffu;
+    const int nitems = per_xcd * kNumXcd;
+    const Deal d = deal_items<kP2Threads>(tot, nb, nitems, wsum);  // synchronises the block
+    if (tid < nb && d.count > 0 && (uint32_t)slot >= d.first && (uint32_t)slot < d.first + d.count) {
+        const uint32_t j = (uint32_t)slot - d.first;
+        s_item[0] = tid;
+        s_item[1] = (int)((unsigned long long)j * ntiles / d.count);
+        s_item[2] = (int)((unsigned long long)(j + 1) * ntiles / d.count);
+    }
+    if (g == 0 && tid < nb) {
+        // the merge pass's view: every bucket's slots, and (home modes) the XCD of its first
+        buckets[tid] = HistBucket{(int)d.first, (int)d.count};
+        if (mode != XD_MODE_OBLIVIOUS)
+            atomicMin(&xfirst[min((int)(d.first / (uint32_t)per_xcd), kNumXcd - 1)], (uint32_t)tid);
+    }
     uint4 *h4 = reinterpret_cast<uint4 *>(h);
     for (int i = tid; i < (int)(kBucketBins / 4) + 1; i += kP2Threads) h4[i] = make_uint4(0, 0, 0, 0);
     __syncthreads();
-
-    const int b = it.bucket;
+    if (g == 0 && tid < kNumXcd) {
+        if (mode == XD_MODE_OBLIVIOUS) {  // merge ranges: equal bucket counts
+            xcd_range[2 * tid] = (int)((long long)tid * nb / kNumXcd);
+            xcd_range[2 * tid + 1] = (int)((long long)(tid + 1) * nb / kNumXcd);
+        } else {
+            // [first bucket of XCD x, first bucket of the next non-empty XCD)
+            int b0 = (xfirst[tid] == 0xffffffffu) ? nb : (int)xfirst[tid];
+            int b1 = nb;
+            for (int y = tid + 1; y < kNumXcd; ++y)
+                if (xfirst[y] != 0xffffffffu) {
+                    b1 = (int)xfirst[y];
+                    break;
+                }
+            if (b0 > b1) b0 = b1;
+            xcd_range[2 * tid] = b0;
+            xcd_range[2 * tid + 1] = b1;
+        }
+    }
+    const int b = s_item[0];
+    if (b < 0) return;  // an idle slot (uniform over the block)
+    struct {
+        int t0, t1;
+    } const it{s_item[1], s_item[2]};
     uint32_t hot = kTrash + 1;  // no hot key yet
     uint32_t hc = 0;
     auto flush_hot = [&]() {
@@ -560,7 +548,7 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     }
     if (hot < kTrash) flush_hot();
     __syncthreads();
-    uint4 *dst = reinterpret_cast<uint4 *>(partials + (size_t)item * kBucketBins);
+    uint4 *dst = reinterpret_cast<uint4 *>(partials + (size_t)slot * kBucketBins);
     for (int i = tid; i < (int)(kBucketBins / 4); i += kP2Threads) dst[i] = h4[i];
 }
 
@@ -647,7 +635,6 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     uint16_t *part = reinterpret_cast<uint16_t *>(ws + L.part);
     uint32_t *offs = reinterpret_cast<uint32_t *>(ws + L.offs);
     uint32_t *tot = reinterpret_cast<uint32_t *>(ws + L.tot);
-    HistItem *items = reinterpret_cast<HistItem *>(ws + L.items);
     HistBucket *buckets = reinterpret_cast<HistBucket *>(ws + L.buckets);
     int *xcdr = reinterpret_cast<int *>(ws + L.xcdr);
     uint32_t *partials = reinterpret_cast<uint32_t *>(ws + L.partials);
@@ -712,15 +699,9 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     }
     if (ntl > L.ntiles) return fail(XD_ERR_WORKSPACE, "xd_hist_u32: tile count exceeds the workspace layout");
     {
-    KernelTimer kt("hist_plan", s);
-    hipLaunchKernelGGL(hist_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, tot, L.nb, ntl, L.per_xcd, mode, items,
-                       buckets, xcdr);
-    if (int rc = launch_status("hist_plan_kernel")) return rc;
-    }
-    {
     KernelTimer kt("hist_count", s);
-    hipLaunchKernelGGL(hist_count_kernel, dim3(L.nitems), dim3(kP2Threads), 0, s, part, offs, L.nb, items, L.per_xcd,
-                       partials, mode, rot_eff);
+    hipLaunchKernelGGL(hist_count_kernel, dim3(L.nitems), dim3(kP2Threads), 0, s, part, offs, L.nb, ntl, tot,
+                       L.per_xcd, partials, buckets, xcdr, mode, rot_eff);
     if (int rc = launch_status("hist_count_kernel")) return rc;
     }
     KernelTimer kt("hist_merge", s);

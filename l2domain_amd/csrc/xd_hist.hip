@@ -377,23 +377,28 @@ __device__ Deal deal_items(const uint32_t *__restrict__ tot, int nb, int nitems,
 // ---------------------------------------------------------------------------------------
 // 3. count
 // ---------------------------------------------------------------------------------------
-constexpr uint32_t kTrash = kBucketBins;  // LDS slot that absorbs elements outside a run
+constexpr uint32_t kTrash = kBucketBins;  // first LDS slot past the bins (hot-key sentinel above it)
+constexpr uint32_t kLaneTrash = kBucketBins + 4;  // lane l's private slot kLaneTrash + l absorbs its dropped keys
+constexpr uint32_t kCountSlots = kLaneTrash + kWave;
 
 // Counts the 8 u16 keys of one 16-byte vector whose first element has index `e`, for the
 // run [s0, e0). Keys equal to the wave's current hot key go to the per-lane register
 // counter `hc` (the hot key of a Zipf bucket would otherwise make most lanes of a wave
-// hit one LDS address); all others take one ds_add each.
+// hit one LDS address). Every key takes one ds_add, with no branch: keys outside the run
+// and hot keys are added to the lane's private trash slot `trash`, so the adds of one
+// instruction never meet on a dropped key's address.
 __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t e, uint32_t s0, uint32_t e0,
-                                          uint32_t hot, uint32_t &hc) {
+                                          uint32_t hot, uint32_t &hc, uint32_t trash) {
     if (e >= e0 || e + 8 <= s0) return;  // vector outside the run (most lanes' 2nd vector)
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
     const uint32_t len = e0 - s0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         uint32_t key = (k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu);
-        key = (e + (uint32_t)k - s0 < len) ? key : kTrash;
-        if (key == hot) ++hc;
-        else atomicAdd(&h[key], 1u);
+        key = (e + (uint32_t)k - s0 < len) ? key : trash;
+        const bool hk = key == hot;  // a trash slot is never the hot key
+        hc += hk ? 1u : 0u;
+        atomicAdd(&h[hk ? trash : key], 1u);
     }
 }
 
@@ -401,7 +406,7 @@ __global__ void __launch_bounds__(kP2Threads)
 hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb, int ntiles,
                   const uint32_t *__restrict__ tot, int per_xcd, uint32_t *__restrict__ partials,
                   HistBucket *__restrict__ buckets, int *__restrict__ xcd_range, int mode, unsigned rot) {
-    __shared__ __attribute__((aligned(16))) uint32_t h[kBucketBins + 4];
+    __shared__ __attribute__((aligned(16))) uint32_t h[kCountSlots];
     __shared__ uint32_t wsum[kP2Waves];
     __shared__ int s_item[3];  // bucket (-1: idle slot), t0, t1
     __shared__ uint32_t xfirst[kNumXcd];
@@ -431,7 +436,7 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
             atomicMin(&xfirst[min((int)(d.first / (uint32_t)per_xcd), kNumXcd - 1)], (uint32_t)tid);
     }
     uint4 *h4 = reinterpret_cast<uint4 *>(h);
-    for (int i = tid; i < (int)(kBucketBins / 4) + 1; i += kP2Threads) h4[i] = make_uint4(0, 0, 0, 0);
+    for (int i = tid; i < (int)(kCountSlots / 4); i += kP2Threads) h4[i] = make_uint4(0, 0, 0, 0);
     __syncthreads();
     if (g == 0 && tid < kNumXcd) {
         if (mode == XD_MODE_OBLIVIOUS) {  // merge ranges: equal bucket counts
@@ -534,8 +539,8 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
                     }
                 }
             }
-            count_vec(h, qa, ea, sa, xa, hot, hc);
-            count_vec(h, qb, eb, sb, xb, hot, hc);
+            count_vec(h, qa, ea, sa, xa, hot, hc, kLaneTrash + (uint32_t)lane);
+            count_vec(h, qb, eb, sb, xb, hot, hc, kLaneTrash + (uint32_t)lane);
             qa = na;
             qb = nb2;
             ea = fa;

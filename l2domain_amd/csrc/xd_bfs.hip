@@ -12,12 +12,14 @@
 // MI355X design.
 //   state: level[V]; a visited bitmap and three rotating frontier bitmaps (u64 words, 512 KiB
 //   each at 2^22 vertices, resident in every XCD's L2); two frontier queues; a control block.
-//   Every level writes the next frontier as a bitmap, and a top-down level also as a queue; a
-//   bottom-up level followed by a top-down one is converted to a queue by one extra pass.
-//   Each level zeroes the bitmap the level after it will fill.
+//   Every level writes the next frontier as a bitmap only; before a top-down level the
+//   bitmap is converted to that level's queue by one pass (a workgroup per 1024 words, one
+//   atomic per workgroup, vertices in ascending order). Appending the winners of a top-down
+//   level to a queue as they claim costs one atomic per wave on a single counter, which
+//   serialises (a hub's expansion took 54 us of a 260 us search). Each level zeroes the
+//   bitmap the level after it will fill.
 //   top-down: one lane per frontier vertex (hubs above kBigDeg are expanded by the whole
-//     grid in a second kernel); a claim is a 64-bit atomicOr on the visited word; winners
-//     are appended to the next queue with one atomicAdd per wave (ballot + mbcnt).
+//     grid in a second kernel); a claim is a 64-bit atomicOr on the visited word.
 //   bottom-up: every unvisited vertex scans its neighbours until one is in the frontier
 //     bitmap; a wave covers one 64-vertex block, i.e. exactly one bitmap word, so it updates
 //     its visited and next words with plain stores. Oblivious mode walks the blocks in order;
@@ -58,7 +60,6 @@ struct BfsCtl {
     long long m_f;  // frontier edges
     long long m_u;  // edges of unvisited vertices
     long long reached_v, reached_e;
-    unsigned long long next_count;  // vertices appended to the next queue in this level
     unsigned long long big_count;   // hub vertices deferred to the grid-wide expansion
     int32_t convert;                // 1: a bottom-up level is followed by a top-down one
     int32_t pad;
@@ -188,31 +189,15 @@ __device__ __forceinline__ bool claim(unsigned long long *visited, uint32_t *lev
     return true;
 }
 
-// Appends the lanes' vertices with won == true to `queue` with one atomic per wave.
-__device__ __forceinline__ void wave_append(bool won, int32_t v, int32_t *queue, unsigned long long *count) {
-    const uint64_t m = __ballot(won);
-    if (!m) return;
-    const int leader = __builtin_ctzll(m);
-    unsigned long long base = 0;
-    if (lane_id() == leader) base = atomicAdd(count, (unsigned long long)__builtin_popcountll(m));
-    base = __shfl(base, leader, kWave);
-    if (won) queue[base + mask_rank(m)] = v;
-}
-
-// A top-down claim of v by this lane: level, visited, next bitmap and next queue.
+// A top-down claim of v by this lane: level, visited and next bitmap.
 __device__ __forceinline__ void td_visit(const BfsState &st, bool have, int32_t v, uint32_t lvl,
-                                         unsigned long long *next_bits, int32_t *next_q,
-                                         unsigned long long &my_verts, unsigned long long &my_edges) {
-    bool won = false;
-    if (have) {
-        won = claim(st.visited, st.level, v, lvl);
-        if (won) {
-            atomicOr(&next_bits[v >> 6], 1ull << (v & 63));
-            my_verts += 1;
-            my_edges += (unsigned long long)(st.rowptr[v + 1] - st.rowptr[v]);
-        }
+                                         unsigned long long *next_bits, unsigned long long &my_verts,
+                                         unsigned long long &my_edges) {
+    if (have && claim(st.visited, st.level, v, lvl)) {
+        atomicOr(&next_bits[v >> 6], 1ull << (v & 63));
+        my_verts += 1;
+        my_edges += (unsigned long long)(st.rowptr[v + 1] - st.rowptr[v]);
     }
-    wave_append(won, v, next_q, &st.ctl->next_count);
 }
 
 // Bottom-up over the 64-vertex block starting at v0 (a multiple of 64): exactly bitmap word
@@ -261,7 +246,6 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
     unsigned long long *next_bits = st.front[(depth + 1) % 3];
     unsigned long long *later_bits = st.front[(depth + 2) % 3];
     const int32_t *cur_q = st.queue[depth & 1];
-    int32_t *next_q = st.queue[(depth + 1) & 1];
     const int64_t tstride = (int64_t)gridDim.x * blockDim.x;
     const int64_t tid0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (int64_t w = tid0; w < st.words; w += tstride) later_bits[w] = 0ull;  // filled by the next level
@@ -271,31 +255,16 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
     constexpr int kWavesPerWg = kBfsThreads / kWave;
     if (dir == kTopDown) {
         const int64_t count = st.ctl->n_f;
-        // Uniform trip count per wave so that the ballots in wave_append see whole waves.
-        const int64_t first = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~(kWave - 1));
-        for (int64_t i0 = first; i0 < count; i0 += tstride) {
-            const int64_t i = i0 + lane_id();
-            int32_t beg = 0, end = 0;
-            if (i < count) {
-                const int32_t u = cur_q[i];
-                beg = st.rowptr[u];
-                end = st.rowptr[u + 1];
-                if (end - beg > kBigDeg) {
-                    const unsigned long long slot = atomicAdd(&st.ctl->big_count, 1ull);
-                    st.big[slot] = u;
-                    end = beg;
-                }
+        for (int64_t i = tid0; i < count; i += tstride) {
+            const int32_t u = cur_q[i];
+            const int32_t beg = st.rowptr[u];
+            int32_t end = st.rowptr[u + 1];
+            if (end - beg > kBigDeg) {  // a hub: expanded by the whole grid in bfs_hubs_kernel
+                const unsigned long long slot = atomicAdd(&st.ctl->big_count, 1ull);
+                st.big[slot] = u;
+                end = beg;
             }
-            // lanes walk their own lists; iterations stay wave-uniform up to the longest list
-            const int32_t len = end - beg;
-            int32_t maxlen = len;
-#pragma unroll
-            for (int d = 32; d >= 1; d >>= 1) maxlen = max(maxlen, __shfl_xor(maxlen, d, kWave));
-            for (int32_t j = 0; j < maxlen; ++j) {
-                const bool have = j < len;
-                const int32_t v = have ? st.col[beg + j] : 0;
-                td_visit(st, have, v, lvl, next_bits, next_q, my_verts, my_edges);
-            }
+            for (int32_t j = beg; j < end; ++j) td_visit(st, true, st.col[j], lvl, next_bits, my_verts, my_edges);
         }
     } else if (mode == XD_MODE_OBLIVIOUS) {
         for (int64_t blk = (int64_t)blockIdx.x * kWavesPerWg + wave; blk < nblocks;
@@ -329,19 +298,13 @@ __global__ void __launch_bounds__(kBfsThreads) bfs_hubs_kernel(BfsState st) {
     const int depth = st.ctl->depth;
     const uint32_t lvl = (uint32_t)depth + 1;
     unsigned long long *next_bits = st.front[(depth + 1) % 3];
-    int32_t *next_q = st.queue[(depth + 1) & 1];
     unsigned long long my_verts = 0, my_edges = 0;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const int64_t first = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~(kWave - 1));
+    const int64_t first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (int64_t h = 0; h < nbig; ++h) {
         const int32_t u = st.big[h];
         const int32_t beg = st.rowptr[u], end = st.rowptr[u + 1];
-        for (int64_t e0 = beg + first; e0 < end; e0 += stride) {
-            const int64_t e = e0 + lane_id();
-            const bool have = e < end;
-            const int32_t v = have ? st.col[e] : 0;
-            td_visit(st, have, v, lvl, next_bits, next_q, my_verts, my_edges);
-        }
+        for (int64_t e = beg + first; e < end; e += stride) td_visit(st, true, st.col[e], lvl, next_bits, my_verts, my_edges);
     }
     block_sum2(my_verts, my_edges);
     if (threadIdx.x == 0) {  // added to the level kernel's partial of the same index
@@ -368,7 +331,6 @@ __global__ void __launch_bounds__(kBfsThreads) bfs_control_kernel(BfsState st, i
     c->depth += 1;
     c->n_f = (long long)v;
     c->m_f = (long long)e;
-    c->next_count = 0;
     c->big_count = 0;
     c->convert = 0;
     c->conv_count = 0;
@@ -381,16 +343,14 @@ __global__ void __launch_bounds__(kBfsThreads) bfs_control_kernel(BfsState st, i
     c->m_u -= (long long)e;
     if (dir == kTopDown) {
         if ((double)c->m_f > (double)c->m_u / kAlpha) c->dir = kBottomUp;
-    } else {
-        if ((double)c->n_f < (double)st.V / kBeta) {
-            c->dir = kTopDown;
-            c->convert = 1;  // the new frontier exists only as a bitmap
-        }
+    } else if ((double)c->n_f < (double)st.V / kBeta) {
+        c->dir = kTopDown;
     }
+    c->convert = c->dir == kTopDown ? 1 : 0;  // the new frontier exists only as a bitmap
 }
 
-// Bitmap -> queue for a top-down level that follows a bottom-up one: the frontier bitmap of
-// the coming level becomes its queue. A workgroup takes a contiguous range of words and
+// Bitmap -> queue before every top-down level: the frontier bitmap of the coming level becomes
+// its queue, in ascending vertex order. A workgroup takes a contiguous range of words and
 // reserves its queue space with one atomic.
 constexpr int kConvWordsPerWg = 1024;
 __global__ void __launch_bounds__(kBfsThreads) bfs_b2q_kernel(BfsState st) {

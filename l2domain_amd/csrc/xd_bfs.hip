@@ -200,6 +200,55 @@ __device__ __forceinline__ void td_visit(const BfsState &st, bool have, int32_t 
     }
 }
 
+// Top-down claims of up to 64 consecutive entries of one adjacency list, one per lane (lanes
+// without an entry have have == false). Lanes whose vertices share a visited word form
+// contiguous runs when the list is sorted, as a hub's lists are here: a segmented OR across
+// each run gathers the bits that still look clear, the run's last lane claims them with one
+// atomicOr and sets the won ones in the next bitmap with one more, and every lane learns from
+// the returned word whether it won (the first lane holding a bit, should a list repeat a
+// vertex). Unsorted lists only make the runs shorter.
+__device__ __forceinline__ void td_visit_runs(const BfsState &st, bool have, int32_t v, uint32_t lvl,
+                                              unsigned long long *next_bits, unsigned long long &my_verts,
+                                              unsigned long long &my_edges) {
+    const int lane = lane_id();
+    const int32_t w = have ? (v >> 6) : -1 - lane;  // a lane without an entry is a run of its own
+    const unsigned long long bit = have ? 1ull << (v & 63) : 0ull;
+    const unsigned long long cur =
+        __hip_atomic_load(st.visited + (have ? w : 0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const unsigned long long mine = (cur & bit) ? 0ull : bit;
+    const bool head = lane == 0 || __shfl_up(w, 1, kWave) != w;
+    const uint64_t heads = __ballot(head);
+    unsigned long long x = mine;  // OR of `mine` from the run's head to this lane
+    bool f = head;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const unsigned long long y = __shfl_up(x, d, kWave);
+        const bool fy = __shfl_up(f ? 1 : 0, d, kWave) != 0;
+        if (lane >= d) {
+            if (!f) x |= y;
+            f = f || fy;
+        }
+    }
+    const unsigned long long before = head ? 0ull : __shfl_up(x, 1, kWave);  // earlier lanes of the run
+    const unsigned long long rest = lane == kWave - 1 ? 0ull : (heads >> (lane + 1));
+    const bool tail = rest & 1ull || lane == kWave - 1;
+    unsigned long long old = 0;
+    if (tail && x) old = atomicOr(st.visited + w, x);
+    const int tl = rest ? lane + __builtin_ctzll(rest) : kWave - 1;  // the run's last lane
+    const unsigned long long run_old = __shfl(old, tl, kWave);
+    if (mine & ~before & ~run_old) {
+        st.level[v] = lvl;
+        my_edges += (unsigned long long)(st.rowptr[v + 1] - st.rowptr[v]);
+    }
+    if (tail && x) {
+        const unsigned long long won = x & ~old;
+        if (won) {
+            atomicOr(&next_bits[w], won);
+            my_verts += (unsigned long long)__builtin_popcountll(won);
+        }
+    }
+}
+
 // Bottom-up over the 64-vertex block starting at v0 (a multiple of 64): exactly bitmap word
 // v0 / 64, which no other wave touches during this level.
 __device__ __forceinline__ void bu_block(const BfsState &st, int32_t v0, const unsigned long long *front,
@@ -300,11 +349,18 @@ __global__ void __launch_bounds__(kBfsThreads) bfs_hubs_kernel(BfsState st) {
     unsigned long long *next_bits = st.front[(depth + 1) % 3];
     unsigned long long my_verts = 0, my_edges = 0;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    const int64_t first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    // every wave takes 64 consecutive list entries at a time (a wave-uniform loop: the runs
+    // of td_visit_runs need whole waves)
+    const int64_t first = (int64_t)blockIdx.x * blockDim.x + (threadIdx.x & ~(kWave - 1));
     for (int64_t h = 0; h < nbig; ++h) {
         const int32_t u = st.big[h];
         const int32_t beg = st.rowptr[u], end = st.rowptr[u + 1];
-        for (int64_t e = beg + first; e < end; e += stride) td_visit(st, true, st.col[e], lvl, next_bits, my_verts, my_edges);
+        for (int64_t e0 = beg + first; e0 < end; e0 += stride) {
+            const int64_t e = e0 + lane_id();
+            const bool have = e < end;
+            const int32_t v = st.col[have ? e : end - 1];
+            td_visit_runs(st, have, v, lvl, next_bits, my_verts, my_edges);
+        }
     }
     block_sum2(my_verts, my_edges);
     if (threadIdx.x == 0) {  // added to the level kernel's partial of the same index

@@ -216,26 +216,34 @@ __device__ __forceinline__ void td_visit_runs(const BfsState &st, bool have, int
     const unsigned long long cur =
         __hip_atomic_load(st.visited + (have ? w : 0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     const unsigned long long mine = (cur & bit) ? 0ull : bit;
-    const bool head = lane == 0 || __shfl_up(w, 1, kWave) != w;
+    // Every shuffle runs on the whole wave and its result is pinned by an empty asm: left to
+    // itself the compiler sinks a shuffle feeding a `||` or `?:` into the branch that needs
+    // it, where the lanes it reads from are switched off and read as 0.
+    int32_t wu = __shfl_up(w, 1, kWave);
+    asm volatile("" : "+v"(wu));
+    const bool head = (lane == 0) | (wu != w);
     const uint64_t heads = __ballot(head);
     unsigned long long x = mine;  // OR of `mine` from the run's head to this lane
     bool f = head;
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
-        const unsigned long long y = __shfl_up(x, d, kWave);
-        const bool fy = __shfl_up(f ? 1 : 0, d, kWave) != 0;
-        if (lane >= d) {
-            if (!f) x |= y;
-            f = f || fy;
-        }
+        unsigned long long y = __shfl_up(x, d, kWave);
+        int fy = __shfl_up(f ? 1 : 0, d, kWave);
+        asm volatile("" : "+v"(y), "+v"(fy));
+        const bool on = lane >= d;
+        x = (on & !f) ? (x | y) : x;
+        f = f | (on & (fy != 0));
     }
-    const unsigned long long before = head ? 0ull : __shfl_up(x, 1, kWave);  // earlier lanes of the run
+    unsigned long long xu = __shfl_up(x, 1, kWave);
+    asm volatile("" : "+v"(xu));
+    const unsigned long long before = head ? 0ull : xu;  // earlier lanes of the run
     const unsigned long long rest = lane == kWave - 1 ? 0ull : (heads >> (lane + 1));
     const bool tail = rest & 1ull || lane == kWave - 1;
     unsigned long long old = 0;
     if (tail && x) old = atomicOr(st.visited + w, x);
     const int tl = rest ? lane + __builtin_ctzll(rest) : kWave - 1;  // the run's last lane
-    const unsigned long long run_old = __shfl(old, tl, kWave);
+    unsigned long long run_old = __shfl(old, tl, kWave);
+    asm volatile("" : "+v"(run_old));
     if (mine & ~before & ~run_old) {
         st.level[v] = lvl;
         my_edges += (unsigned long long)(st.rowptr[v + 1] - st.rowptr[v]);

@@ -68,6 +68,31 @@ def test_shapes(mode):
     assert st["bottomup_steps"] >= 1
 
 
+@pytest.mark.parametrize("mode", MODES)
+def test_hub_list_unsorted_with_repeats(mode):
+    # The grid-wide hub expansion gathers claims over runs of lanes sharing a visited word:
+    # every vertex must still be claimed once (level and reached edges exact) when the hub's
+    # list is shuffled and repeats entries.
+    rng = np.random.default_rng(11)
+    V = 12000
+    hub = np.arange(1, 10000, dtype=np.int32)
+    hub = np.concatenate([hub, rng.choice(hub, 700)])
+    rng.shuffle(hub)
+    adj = [hub.tolist()] + [[0] for _ in range(1, 10000)] + [[] for _ in range(10000, V)]
+    for i in range(9999, V - 1):  # a path 9999 - 10000 - ... - 11999 behind the star
+        adj[i].append(i + 1)
+        adj[i + 1].append(i)
+    rowptr = np.zeros(V + 1, dtype=np.int32)
+    rowptr[1:] = np.cumsum([len(a) for a in adj])
+    col = np.array([v for a in adj for v in a], dtype=np.int32)
+    st = check(rowptr, col, 0, mode)
+    assert st["levels"] >= 3
+    # the same hub sorted, repeats kept next to their first copy
+    adj[0] = sorted(adj[0])
+    col = np.array([v for a in adj for v in a], dtype=np.int32)
+    check(rowptr, col, 0, mode)
+
+
 @pytest.fixture(scope="module")
 def config_graph():
     rowptr, col = rmat_csr(RMAT_SCALE, RMAT_EDGE_FACTOR, RMAT_SEED)

@@ -341,7 +341,7 @@ int xd_bfs_route(const int32_t *rowptr, const int32_t *col, int32_t num_vertices
 
 /* level[v] = BFS distance from src, XD_BFS_UNVISITED (0xFFFFFFFF) if unreachable, for the
  * undirected graph rowptr[V+1] / col[nnz] (int32, device; every edge stored both ways).
- * Direction-optimizing (top-down queue steps, bottom-up bitmap steps, Beamer's switch with
+ * Direction-optimizing (top-down and bottom-up steps over frontier bitmaps, Beamer's switch with
  * alpha = 14 and beta = 24, decided on the device; the host reads the control block after six
  * levels and then after every four). Replaces luo_baseline_level_kernel / luo_side_level_kernel and the host
  * level loops (applications/bfs/src/bfs.cu:215-308, 449-491), which run a fixed number of

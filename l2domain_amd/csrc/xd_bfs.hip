@@ -11,15 +11,16 @@
 //
 // MI355X design.
 //   state: level[V]; a visited bitmap and three rotating frontier bitmaps (u64 words, 512 KiB
-//   each at 2^22 vertices, resident in every XCD's L2); two frontier queues; a control block.
-//   Every level writes the next frontier as a bitmap only; before a top-down level the
-//   bitmap is converted to that level's queue by one pass (a workgroup per 1024 words, one
-//   atomic per workgroup, vertices in ascending order). Appending the winners of a top-down
-//   level to a queue as they claim costs one atomic per wave on a single counter, which
-//   serialises (a hub's expansion took 54 us of a 260 us search). Each level zeroes the
-//   bitmap the level after it will fill.
-//   top-down: one lane per frontier vertex (hubs above kBigDeg are expanded by the whole
-//     grid in a second kernel); a claim is a 64-bit atomicOr on the visited word.
+//   each at 2^22 vertices, resident in every XCD's L2); a control block. There is no frontier
+//   queue: every level writes the next frontier as a bitmap only, and a top-down level reads
+//   its frontier from the bitmap. (Appending the winners of a top-down level to a queue as
+//   they claim costs one atomic per wave on a single counter, which serialises: a hub's
+//   expansion took 54 us of a 260 us search; a conversion pass from bitmap to queue before
+//   every top-down level cost a launch per level.) Each level zeroes the bitmap the level
+//   after it will fill.
+//   top-down: a wave per frontier bitmap word, lane l expanding vertex 64 w + l when its bit
+//     is set (hubs above kBigDeg are expanded by the whole grid in a second kernel); a claim
+//     is a 64-bit atomicOr on the visited word.
 //   bottom-up: every unvisited vertex scans its neighbours until one is in the frontier
 //     bitmap; a wave covers one 64-vertex block, i.e. exactly one bitmap word, so it updates
 //     its visited and next words with plain stores. Oblivious mode walks the blocks in order;
@@ -29,7 +30,7 @@
 //   direction: top-down -> bottom-up when m_f > m_u / 14, bottom-up -> top-down when
 //     n_f < V / 24 (Beamer, Asanovic, Patterson, SC'12), decided on the device by a
 //     one-workgroup control kernel after every level. The host enqueues levels in batches
-//     (level, hub expansion, control, conversion) of six, then four, and reads the control
+//     (level, hub expansion, control) of six, then four, and reads the control
 //     block once per batch; the
 //     kernels of levels enqueued after the search ended return at once.
 #include <hip/hip_runtime.h>
@@ -56,14 +57,11 @@ struct BfsCtl {
     int32_t dir;    // kTopDown, kBottomUp or kDone
     int32_t depth;  // completed levels; the running level writes depth + 1
     int32_t td_steps, bu_steps;
-    long long n_f;  // frontier vertices (the current queue's length)
+    long long n_f;  // frontier vertices
     long long m_f;  // frontier edges
     long long m_u;  // edges of unvisited vertices
     long long reached_v, reached_e;
-    unsigned long long big_count;   // hub vertices deferred to the grid-wide expansion
-    int32_t convert;                // 1: a bottom-up level is followed by a top-down one
-    int32_t pad;
-    unsigned long long conv_count;  // queue entries written by the bitmap -> queue pass
+    unsigned long long big_count;  // hub vertices deferred to the grid-wide expansion
 };
 
 struct BfsPartial {  // per workgroup, summed by the control kernel
@@ -72,7 +70,7 @@ struct BfsPartial {  // per workgroup, summed by the control kernel
 };
 
 struct BfsLayout {
-    size_t visited, front[3], queue[2], big, ctl, partials, route, total;
+    size_t visited, front[3], big, ctl, partials, route, total;
     int64_t words, nblocks;
 };
 
@@ -98,10 +96,6 @@ static BfsLayout bfs_layout(int32_t V, int64_t nnz) {
         L.front[i] = o;
         o = a256(o + 8 * (size_t)L.words);
     }
-    for (int i = 0; i < 2; ++i) {
-        L.queue[i] = o;
-        o = a256(o + 4 * (size_t)V);
-    }
     L.big = o;
     o = a256(o + 4 * (size_t)V);
     L.route = o;  // per-call block lists when the caller passes no route
@@ -119,7 +113,6 @@ struct BfsState {
     uint32_t *level;
     unsigned long long *visited;
     unsigned long long *front[3];
-    int32_t *queue[2];
     int32_t *big;
     BfsCtl *ctl;
     BfsPartial *parts;
@@ -160,11 +153,10 @@ __global__ void __launch_bounds__(256) bfs_init_kernel(BfsState st, int32_t src,
     for (int64_t w = t0; w < st.words; w += stride) {
         const unsigned long long b = (w == src / 64) ? (1ull << (src % 64)) : 0ull;
         st.visited[w] = b;
-        st.front[0][w] = b;  // level 1 reads front[0] (bottom-up) or queue[0] (top-down)
+        st.front[0][w] = b;  // the first level's frontier: the source
         st.front[1][w] = 0ull;
     }
     if (t0 == 0) {
-        st.queue[0][0] = src;
         const long long deg = st.rowptr[src + 1] - st.rowptr[src];
         BfsCtl c{};
         c.dir = kTopDown;
@@ -302,7 +294,6 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
     const unsigned long long *cur_bits = st.front[depth % 3];
     unsigned long long *next_bits = st.front[(depth + 1) % 3];
     unsigned long long *later_bits = st.front[(depth + 2) % 3];
-    const int32_t *cur_q = st.queue[depth & 1];
     const int64_t tstride = (int64_t)gridDim.x * blockDim.x;
     const int64_t tid0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (int64_t w = tid0; w < st.words; w += tstride) later_bits[w] = 0ull;  // filled by the next level
@@ -311,9 +302,13 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
     const int wave = (int)threadIdx.x / kWave;
     constexpr int kWavesPerWg = kBfsThreads / kWave;
     if (dir == kTopDown) {
-        const int64_t count = st.ctl->n_f;
-        for (int64_t i = tid0; i < count; i += tstride) {
-            const int32_t u = cur_q[i];
+        // a wave per frontier bitmap word: lane l expands vertex 64 w + l when its bit is set
+        const int lane = lane_id();
+        for (int64_t w = (int64_t)blockIdx.x * kWavesPerWg + wave; w < st.words;
+             w += (int64_t)gridDim.x * kWavesPerWg) {
+            const unsigned long long m = cur_bits[w];
+            if (!((m >> lane) & 1ull)) continue;
+            const int32_t u = (int32_t)(w * kWave + lane);
             const int32_t beg = st.rowptr[u];
             int32_t end = st.rowptr[u + 1];
             if (end - beg > kBigDeg) {  // a hub: expanded by the whole grid in bfs_hubs_kernel
@@ -396,8 +391,6 @@ __global__ void __launch_bounds__(kBfsThreads) bfs_control_kernel(BfsState st, i
     c->n_f = (long long)v;
     c->m_f = (long long)e;
     c->big_count = 0;
-    c->convert = 0;
-    c->conv_count = 0;
     if (v == 0) {
         c->dir = kDone;
         return;
@@ -409,62 +402,6 @@ __global__ void __launch_bounds__(kBfsThreads) bfs_control_kernel(BfsState st, i
         if ((double)c->m_f > (double)c->m_u / kAlpha) c->dir = kBottomUp;
     } else if ((double)c->n_f < (double)st.V / kBeta) {
         c->dir = kTopDown;
-    }
-    c->convert = c->dir == kTopDown ? 1 : 0;  // the new frontier exists only as a bitmap
-}
-
-// Bitmap -> queue before every top-down level: the frontier bitmap of the coming level becomes
-// its queue, in ascending vertex order. A workgroup takes a contiguous range of words and
-// reserves its queue space with one atomic.
-constexpr int kConvWordsPerWg = 1024;
-__global__ void __launch_bounds__(kBfsThreads) bfs_b2q_kernel(BfsState st) {
-    if (st.ctl->convert == 0) return;
-    const int depth = st.ctl->depth;
-    const unsigned long long *bits = st.front[depth % 3];
-    int32_t *q = st.queue[depth & 1];
-    __shared__ uint32_t wtot[kBfsThreads / kWave];
-    __shared__ unsigned long long wbase;
-    const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-    for (int64_t w0 = (int64_t)blockIdx.x * kConvWordsPerWg; w0 < st.words;
-         w0 += (int64_t)gridDim.x * kConvWordsPerWg) {
-        // each thread takes 4 consecutive words of the workgroup's 1024
-        unsigned long long m[4];
-        uint32_t c = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t w = w0 + 4 * tid + j;
-            m[j] = w < st.words ? bits[w] : 0ull;
-            c += (uint32_t)__builtin_popcountll(m[j]);
-        }
-        uint32_t incl = c;
-#pragma unroll
-        for (int d = 1; d < kWave; d <<= 1) {
-            const uint32_t t = __shfl_up(incl, d, kWave);
-            if (lane >= d) incl += t;
-        }
-        if (lane == kWave - 1) wtot[wave] = incl;
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t tot = 0;
-            for (int k = 0; k < kBfsThreads / kWave; ++k) {
-                const uint32_t x = wtot[k];
-                wtot[k] = tot;
-                tot += x;
-            }
-            wbase = tot ? atomicAdd(&st.ctl->conv_count, (unsigned long long)tot) : 0ull;
-        }
-        __syncthreads();
-        unsigned long long pos = wbase + wtot[wave] + (incl - c);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            unsigned long long x = m[j];
-            const int64_t w = w0 + 4 * tid + j;
-            while (x) {
-                q[pos++] = (int32_t)(w * 64 + __builtin_ctzll(x));
-                x &= x - 1;
-            }
-        }
-        __syncthreads();
     }
 }
 
@@ -569,7 +506,6 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     st.level = level;
     st.visited = reinterpret_cast<unsigned long long *>(ws + L.visited);
     for (int i = 0; i < 3; ++i) st.front[i] = reinterpret_cast<unsigned long long *>(ws + L.front[i]);
-    for (int i = 0; i < 2; ++i) st.queue[i] = reinterpret_cast<int32_t *>(ws + L.queue[i]);
     st.big = reinterpret_cast<int32_t *>(ws + L.big);
     st.ctl = reinterpret_cast<BfsCtl *>(ws + L.ctl);
     st.parts = reinterpret_cast<BfsPartial *>(ws + L.partials);
@@ -588,7 +524,6 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     const auto *bcount = static_cast<const unsigned long long *>(rt);
     const auto *blist =
         rt ? reinterpret_cast<const int32_t *>(static_cast<const char *>(rt) + kRouteHeader) : nullptr;
-    const unsigned conv_grid = (unsigned)std::min<int64_t>(512, (L.words + kConvWordsPerWg - 1) / kConvWordsPerWg);
     BfsCtl h{};
     for (int64_t enq = 0;;) {
         const int batch = enq == 0 ? kFirstBatch : kLevelBatch;
@@ -600,7 +535,6 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
             }
             hipLaunchKernelGGL(bfs_hubs_kernel, dim3(kBigGrid), dim3(kBfsThreads), 0, s, st);
             hipLaunchKernelGGL(bfs_control_kernel, dim3(1), dim3(kBfsThreads), 0, s, st, kBfsGrid);
-            hipLaunchKernelGGL(bfs_b2q_kernel, dim3(conv_grid), dim3(kBfsThreads), 0, s, st);
             if (int rc = launch_status("bfs level kernels")) return rc;
         }
         XD_HIP(hipMemcpyAsync(&h, st.ctl, sizeof(h), hipMemcpyDeviceToHost, s));

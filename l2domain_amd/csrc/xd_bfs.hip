@@ -249,37 +249,69 @@ __device__ __forceinline__ void td_visit_runs(const BfsState &st, bool have, int
     }
 }
 
-// Bottom-up over the 64-vertex block starting at v0 (a multiple of 64): exactly bitmap word
-// v0 / 64, which no other wave touches during this level.
-__device__ __forceinline__ void bu_block(const BfsState &st, int32_t v0, const unsigned long long *front,
-                                         unsigned long long *next_bits, uint32_t lvl,
-                                         unsigned long long &my_verts, unsigned long long &my_edges) {
+// Bottom-up over two 64-vertex blocks starting at v0a and v0b (multiples of 64; the second
+// only if hasb): exactly bitmap words v0a / 64 and v0b / 64, which no other wave touches
+// during this level. Every lane scans the lists of its vertex in both blocks together, so
+// two chains of (list entry, frontier word) loads are in flight, until it finds a neighbour
+// in the frontier or runs out of neighbours. Loads are unconditional (a finished chain reads
+// entry 0, which exists whenever a chain is active), so no load sits under a branch.
+__device__ __forceinline__ void bu_blocks(const BfsState &st, int32_t v0a, int32_t v0b, bool hasb,
+                                          const unsigned long long *front, unsigned long long *next_bits,
+                                          uint32_t lvl, unsigned long long &my_verts, unsigned long long &my_edges) {
     const int lane = lane_id();
-    const int32_t v = v0 + lane;
-    const int32_t w0 = v0 >> 6;
-    const unsigned long long vis = st.visited[w0];
-    bool found = false;
-    int32_t deg = 0;
-    if (v < st.V && !((vis >> lane) & 1ull)) {
-        const int32_t beg = st.rowptr[v], end = st.rowptr[v + 1];
-        deg = end - beg;
-        for (int32_t e = beg; e < end; ++e) {
-            const int32_t u = st.col[e];
-            if ((front[u >> 6] >> (u & 63)) & 1ull) {
-                found = true;
-                break;
-            }
-        }
+    const int32_t va = v0a + lane, vb = v0b + lane;
+    const int32_t wa = v0a >> 6, wb = v0b >> 6;
+    const unsigned long long visa = st.visited[wa];
+    const unsigned long long visb = st.visited[hasb ? wb : wa];
+    bool ta = va < st.V && !((visa >> lane) & 1ull);  // still searching
+    bool tb = hasb && vb < st.V && !((visb >> lane) & 1ull);
+    const int32_t ia = ta ? va : 0, ib = tb ? vb : 0;
+    int32_t ea = st.rowptr[ia], eb = st.rowptr[ib];
+    int32_t ra = st.rowptr[ia + 1], rb = st.rowptr[ib + 1];
+    asm volatile("" : "+v"(ea), "+v"(eb), "+v"(ra), "+v"(rb));
+    const int32_t enda = ta ? ra : ea, endb = tb ? rb : eb;
+    const int32_t dega = enda - ea, degb = endb - eb;
+    bool fa = false, fb = false;
+    for (;;) {
+        const bool aa = ta && ea < enda, ab = tb && eb < endb;
+        if (!(aa | ab)) break;
+        // both chains' loads on every lane, pinned so the compiler cannot sink either under its
+        // chain's condition (which would serialise the two chains again)
+        int32_t ua = st.col[aa ? ea : 0];
+        int32_t ub = st.col[ab ? eb : 0];
+        asm volatile("" : "+v"(ua), "+v"(ub));
+        unsigned long long fwa = front[ua >> 6];
+        unsigned long long fwb = front[ub >> 6];
+        asm volatile("" : "+v"(fwa), "+v"(fwb));
+        const bool ha = aa && ((fwa >> (ua & 63)) & 1ull);
+        const bool hb = ab && ((fwb >> (ub & 63)) & 1ull);
+        fa = fa | ha;
+        fb = fb | hb;
+        ta = ta && !ha;
+        tb = tb && !hb;
+        ea += aa ? 1 : 0;
+        eb += ab ? 1 : 0;
     }
-    if (found) {
-        st.level[v] = lvl;
+    if (fa) {
+        st.level[va] = lvl;
         my_verts += 1;
-        my_edges += (unsigned long long)deg;
+        my_edges += (unsigned long long)dega;
     }
-    const uint64_t m = __ballot(found);
-    if (m && lane == 0) {
-        st.visited[w0] = vis | m;
-        next_bits[w0] = m;
+    if (fb) {
+        st.level[vb] = lvl;
+        my_verts += 1;
+        my_edges += (unsigned long long)degb;
+    }
+    const uint64_t ma = __ballot(fa), mb = __ballot(fb);
+    if (lane == 0) {
+        if (ma) {
+            st.visited[wa] = visa | ma;
+            next_bits[wa] = ma;
+        }
+        if (mb) {
+            st.visited[wb] = visb | mb;
+            next_bits[wb] = mb;
+        }
     }
 }
 
@@ -319,9 +351,12 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
             for (int32_t j = beg; j < end; ++j) td_visit(st, true, st.col[j], lvl, next_bits, my_verts, my_edges);
         }
     } else if (mode == XD_MODE_OBLIVIOUS) {
-        for (int64_t blk = (int64_t)blockIdx.x * kWavesPerWg + wave; blk < nblocks;
-             blk += (int64_t)gridDim.x * kWavesPerWg)
-            bu_block(st, (int32_t)(blk * kWave), cur_bits, next_bits, lvl, my_verts, my_edges);
+        const int64_t bstride = (int64_t)gridDim.x * kWavesPerWg;
+        for (int64_t blk = (int64_t)blockIdx.x * kWavesPerWg + wave; blk < nblocks; blk += 2 * bstride) {
+            const bool hasb = blk + bstride < nblocks;
+            bu_blocks(st, (int32_t)(blk * kWave), (int32_t)((hasb ? blk + bstride : blk) * kWave), hasb, cur_bits,
+                      next_bits, lvl, my_verts, my_edges);
+        }
     } else {
         // The workgroups of a die walk that die's block list (aware) or the other die's
         // (rotated), so the neighbour lists are read from the near (far) die.
@@ -332,8 +367,12 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
         const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
         const int32_t *mine = blist + (int64_t)want * nblocks;
         const int64_t cnt = (int64_t)bcount[want];
-        for (int64_t i = (int64_t)rank * kWavesPerWg + wave; i < cnt; i += (int64_t)per_die * kWavesPerWg)
-            bu_block(st, mine[i] * kWave, cur_bits, next_bits, lvl, my_verts, my_edges);
+        const int64_t istride = (int64_t)per_die * kWavesPerWg;
+        for (int64_t i = (int64_t)rank * kWavesPerWg + wave; i < cnt; i += 2 * istride) {
+            const bool hasb = i + istride < cnt;
+            bu_blocks(st, mine[i] * kWave, mine[hasb ? i + istride : i] * kWave, hasb, cur_bits, next_bits, lvl,
+                      my_verts, my_edges);
+        }
     }
     block_sum2(my_verts, my_edges);
     if (threadIdx.x == 0) {

@@ -382,13 +382,14 @@ constexpr uint32_t kLaneTrash = kBucketBins + 4;  // lane l's private slot kLane
 constexpr uint32_t kCountSlots = kLaneTrash + kWave;
 
 // Counts the 8 u16 keys of one 16-byte vector whose first element has index `e`, for the
-// run [s0, e0). Keys equal to the wave's current hot key go to the per-lane register
-// counter `hc` (the hot key of a Zipf bucket would otherwise make most lanes of a wave
-// hit one LDS address). Every key takes one ds_add, with no branch: keys outside the run
-// and hot keys are added to the lane's private trash slot `trash`, so the adds of one
+// run [s0, e0). Keys equal to the wave's two current hot keys go to the per-lane register
+// counters `hc` and `hc2` (the hot keys of a Zipf bucket would otherwise make many lanes of
+// a wave hit one LDS address). Every key takes one ds_add, with no branch: keys outside the
+// run and hot keys are added to the lane's private trash slot `trash`, so the adds of one
 // instruction never meet on a dropped key's address.
 __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t e, uint32_t s0, uint32_t e0,
-                                          uint32_t hot, uint32_t &hc, uint32_t trash) {
+                                          uint32_t hot, uint32_t hot2, uint32_t &hc, uint32_t &hc2,
+                                          uint32_t trash) {
     if (e >= e0 || e + 8 <= s0) return;  // vector outside the run (most lanes' 2nd vector)
     const uint32_t w[4] = {q.x, q.y, q.z, q.w};
     const uint32_t len = e0 - s0;
@@ -396,9 +397,10 @@ __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t 
     for (int k = 0; k < 8; ++k) {
         uint32_t key = (k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu);
         key = (e + (uint32_t)k - s0 < len) ? key : trash;
-        const bool hk = key == hot;  // a trash slot is never the hot key
-        hc += hk ? 1u : 0u;
-        atomicAdd(&h[hk ? trash : key], 1u);
+        const bool h1 = key == hot, h2 = key == hot2;  // a trash slot is never a hot key
+        hc += h1 ? 1u : 0u;
+        hc2 += h2 ? 1u : 0u;
+        atomicAdd(&h[(h1 | h2) ? trash : key], 1u);
     }
 }
 
@@ -461,8 +463,13 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     struct {
         int t0, t1;
     } const it{s_item[1], s_item[2]};
-    uint32_t hot = kTrash + 1;  // no hot key yet
-    uint32_t hc = 0;
+    uint32_t hot = kTrash + 1, hot2 = kTrash + 2;  // no hot keys yet (never equal, never a key)
+    uint32_t hc = 0, hc2 = 0;
+    auto flush_hot2 = [&]() {
+        const uint32_t tot_hot = wave_sum_u32(hc2);
+        if (lane == 0 && tot_hot) atomicAdd(&h[hot2], tot_hot);
+        hc2 = 0;
+    };
     auto flush_hot = [&]() {
         const uint32_t tot_hot = wave_sum_u32(hc);
         if (lane == 0 && tot_hot) atomicAdd(&h[hot], tot_hot);
@@ -524,9 +531,10 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
             uint32_t fa, fb, ta, tb2, ya, yb;
             fetch(G + 2 * kWave, na, fa, ta, ya);
             fetch(G + 3 * kWave, nb2, fb, tb2, yb);
-            // Hot-key vote on the first key of every lane's first vector: keep the current
+            // Hot-key votes on the first key of every lane's first vector: keep the current
             // hot key while a quarter of the samples match it, else adopt the first sample if
-            // a quarter of the samples match that one.
+            // a quarter of the samples match that one; the second hot key likewise among the
+            // other samples, at an eighth. (The votes are wave-uniform.)
             const bool sv = ea - sa < xa - sa;
             const uint32_t sk = qa.x & 0xffffu;
             if (__builtin_popcountll(__ballot(sv && sk == hot)) < kWave / 4) {
@@ -535,12 +543,26 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
                     const uint32_t cand = (uint32_t)__builtin_amdgcn_readlane((int)sk, __builtin_ctzll(svm));
                     if (__builtin_popcountll(__ballot(sv && sk == cand)) >= kWave / 4) {
                         flush_hot();
+                        if (cand == hot2) {
+                            flush_hot2();
+                            hot2 = kTrash + 2;
+                        }
                         hot = cand;
                     }
                 }
             }
-            count_vec(h, qa, ea, sa, xa, hot, hc, kLaneTrash + (uint32_t)lane);
-            count_vec(h, qb, eb, sb, xb, hot, hc, kLaneTrash + (uint32_t)lane);
+            if (__builtin_popcountll(__ballot(sv && sk == hot2)) < kWave / 8) {
+                const uint64_t svm = __ballot(sv && sk != hot);
+                if (svm) {
+                    const uint32_t cand = (uint32_t)__builtin_amdgcn_readlane((int)sk, __builtin_ctzll(svm));
+                    if (__builtin_popcountll(__ballot(sv && sk == cand)) >= kWave / 8) {
+                        flush_hot2();
+                        hot2 = cand;
+                    }
+                }
+            }
+            count_vec(h, qa, ea, sa, xa, hot, hot2, hc, hc2, kLaneTrash + (uint32_t)lane);
+            count_vec(h, qb, eb, sb, xb, hot, hot2, hc, hc2, kLaneTrash + (uint32_t)lane);
             qa = na;
             qb = nb2;
             ea = fa;
@@ -552,6 +574,7 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
         }
     }
     if (hot < kTrash) flush_hot();
+    if (hot2 < kTrash) flush_hot2();
     __syncthreads();
     uint4 *dst = reinterpret_cast<uint4 *>(partials + (size_t)slot * kBucketBins);
     for (int i = tid; i < (int)(kBucketBins / 4); i += kP2Threads) dst[i] = h4[i];

@@ -131,6 +131,7 @@ constexpr int kPackBuckets = kColCounters / kWave;
 constexpr uint32_t kPackSpare = (uint32_t)kPackBuckets << kHB;
 constexpr int kPackShift = 21;
 static_assert(kPackSpare == (1u << (kPackShift - 1)), "packed keys and the spare fit below the slot bits");
+static_assert((kPackSpare >> kHB) * kWave == kColCounters, "the packed spare key's counter row is the spare row");
 static_assert(kP1Threads / kWave * 4 * kP1Vec * (kWave * kPackBuckets / kColCounters) <= (1 << (32 - kPackShift)),
               "packed slots overflow");
 
@@ -239,8 +240,13 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
     __syncthreads();
 
     // Counter index of a key: its bucket's row, this lane's column (a spare key's row is past
-    // the table, so the clamp sends it to this lane's spare counter).
-    auto slot_of = [&](uint32_t key) { return min((key >> kHB) * (uint32_t)S + my_col, kColCounters + my_col); };
+    // the table, so the clamp sends it to this lane's spare counter). Packed (at most
+    // kPackBuckets buckets, so S = kWave): the spare key kPackSpare is bucket kPackBuckets,
+    // whose row is exactly the spare counters, so no clamp is needed.
+    auto slot_of = [&](uint32_t key) -> uint32_t {
+        if (PACK) return ((key >> kHB) * (uint32_t)kWave) | my_col;
+        return min((key >> kHB) * (uint32_t)S + my_col, kColCounters + my_col);
+    };
 
     // Slot of every key inside its column: a returning LDS add. Unpacked, slots stay below
     // kTileKeys <= 2^16, so two share a register.

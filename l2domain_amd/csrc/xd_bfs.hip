@@ -51,6 +51,7 @@ constexpr int32_t kBigDeg = 4096;   // top-down: larger lists are expanded by th
 constexpr double kAlpha = 14.0, kBeta = 24.0;
 constexpr int kFirstBatch = 6;      // levels enqueued before the first host round trip
 constexpr int kLevelBatch = 4;      // levels enqueued per later round trip
+constexpr int kTdWords = 4;         // frontier words a wave loads at once in a top-down level
 constexpr int kTopDown = 0, kBottomUp = 1, kDone = 2;
 
 struct BfsCtl {
@@ -334,21 +335,30 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
     const int wave = (int)threadIdx.x / kWave;
     constexpr int kWavesPerWg = kBfsThreads / kWave;
     if (dir == kTopDown) {
-        // a wave per frontier bitmap word: lane l expands vertex 64 w + l when its bit is set
+        // a wave per frontier bitmap word: lane l expands vertex 64 w + l when its bit is set;
+        // a wave's next kTdWords words are loaded together (one round trip, not one each)
         const int lane = lane_id();
-        for (int64_t w = (int64_t)blockIdx.x * kWavesPerWg + wave; w < st.words;
-             w += (int64_t)gridDim.x * kWavesPerWg) {
-            const unsigned long long m = cur_bits[w];
-            if (!((m >> lane) & 1ull)) continue;
-            const int32_t u = (int32_t)(w * kWave + lane);
-            const int32_t beg = st.rowptr[u];
-            int32_t end = st.rowptr[u + 1];
-            if (end - beg > kBigDeg) {  // a hub: expanded by the whole grid in bfs_hubs_kernel
-                const unsigned long long slot = atomicAdd(&st.ctl->big_count, 1ull);
-                st.big[slot] = u;
-                end = beg;
+        const int64_t wstride = (int64_t)gridDim.x * kWavesPerWg;
+        for (int64_t w0 = (int64_t)blockIdx.x * kWavesPerWg + wave; w0 < st.words; w0 += kTdWords * wstride) {
+            unsigned long long m[kTdWords];
+#pragma unroll
+            for (int k = 0; k < kTdWords; ++k) m[k] = cur_bits[min(w0 + k * wstride, st.words - 1)];
+#pragma unroll
+            for (int k = 0; k < kTdWords; ++k) asm volatile("" : "+v"(m[k]));
+#pragma unroll
+            for (int k = 0; k < kTdWords; ++k) {
+                const int64_t w = w0 + k * wstride;
+                if (w >= st.words || !((m[k] >> lane) & 1ull)) continue;
+                const int32_t u = (int32_t)(w * kWave + lane);
+                const int32_t beg = st.rowptr[u];
+                int32_t end = st.rowptr[u + 1];
+                if (end - beg > kBigDeg) {  // a hub: expanded by the whole grid in bfs_hubs_kernel
+                    const unsigned long long slot = atomicAdd(&st.ctl->big_count, 1ull);
+                    st.big[slot] = u;
+                    end = beg;
+                }
+                for (int32_t j = beg; j < end; ++j) td_visit(st, true, st.col[j], lvl, next_bits, my_verts, my_edges);
             }
-            for (int32_t j = beg; j < end; ++j) td_visit(st, true, st.col[j], lvl, next_bits, my_verts, my_edges);
         }
     } else if (mode == XD_MODE_OBLIVIOUS) {
         const int64_t bstride = (int64_t)gridDim.x * kWavesPerWg;

@@ -1,15 +1,28 @@
 #!/usr/bin/env python3
 """Benchmark of the XCD-domain kernels on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--cold] [--only] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--cold] [--only]
+                [--modes aware,oblivious,rotated] [--no-cpu] [--detail FILE]
 
 A step is one pass of the hot path over one batch of synthetic input already resident in
-HBM: one GEMV call, one histogram of 2^28 keys, ... W untimed warm-up steps, then exactly K
-steps timed with HIP events on the stream the kernels are launched on. Prints ONE JSON line.
-`value` is the XCD-aware variant's throughput; the oblivious and rotated variants are
-timed over the same K steps and reported beside it with the aware/oblivious speedup.
-Unless --only is given, every other configuration (GEMV fp32 and fp16 warm and cold, hash,
-the reference's dependent probe, byte histogram and fixed-depth BFS, BFS) is measured the same way, with at most 50 timed steps, under "extras".
+HBM: one GEMV call, one histogram of 2^28 keys, one hash clear + insert + lookup, one BFS.
+W untimed warm-up steps, then exactly K steps timed with HIP events on the stream the
+kernels are launched on. Prints ONE JSON line: the headline (the
+histogram, XCD-aware) first, then one short entry per other configuration under "configs".
+`value` is the XCD-aware variant's throughput; the oblivious and rotated variants are timed
+over the same K steps and reported beside it with the aware/oblivious speedup.
+
+Rooflines use each kernel's own execution time: the library stamps a start/stop event pair
+on every dispatch (hipExtLaunchKernel) while timing is on, so a duration here is what a
+rocprofv3 kernel trace reports for that kernel. Warm configurations whose data fits the
+Infinity Cache are priced against a read stream of the same footprint measured in the same
+run (bound "infinity_cache"); the rest against the 8 TB/s HBM peak. A cold step flushes
+the L2s and the Infinity Cache first and its throughput is taken from the kernels' own
+durations (the flush and the dispatch gaps are not part of the step).
+
+--detail FILE writes every per-kernel, per-mode duration and the CPU baseline samples as
+JSON; --modes restricts the timed modes (one mode per rocprofv3 run gives one row per
+configuration and mode).
 """
 from __future__ import annotations
 
@@ -27,34 +40,70 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "GEMV GB/s (% HBM peak); hist Gkeys/s; XCD-aware vs oblivious speedup"
 MODES = ("oblivious", "aware", "rotated")
 
+# HBM bytes per launch of each configuration's roofline kernel, XCD-aware mode: rocprofv3
+# --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of that kernel under the same bench
+# command, FETCH_SIZE scaled by the copy-kernel calibration factor (a 256 MiB copy reads
+# 2.000x what FETCH_SIZE counts). Sources: profiles/*_traffic.md.
+TRAFFIC = {}
 
-def _cpu_threads() -> int:
+
+def cpu_threads() -> int:
+    """The host threads a CPU baseline may use: the process's CPU affinity, capped by
+    OMP_NUM_THREADS where the box sets its CPU share there."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
         n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+    share = os.environ.get("OMP_NUM_THREADS")
+    if share and share.isdigit() and int(share) > 0:
+        n = min(n, int(share))
+    return max(1, n)
+
+
+def timed_loop(fn, min_s: float, max_reps: int = 1 << 30) -> tuple[float, int]:
+    """Seconds per call of fn() over at least one call and about min_s seconds."""
+    t0 = time.perf_counter()
+    reps = 0
+    while reps < max_reps:
+        fn()
+        reps += 1
+        if time.perf_counter() - t0 >= min_s:
+            break
+    return (time.perf_counter() - t0) / reps, reps
 
 
 # ---------------------------------------------------------------------------------------
 # Workloads
 # ---------------------------------------------------------------------------------------
-class GemvF32:
-    single_kernel = True  # a step is exactly one launch: the timed region gives its duration
+class Workload:
+    single_kernel = False  # a step is exactly one launch
+    ic_resident = False    # warm data fits the 256 MB Infinity Cache
+    cpu_parallel = True    # the CPU restatement has a multi-threaded form
+    roof_bytes = 0         # algorithmic bytes per launch of the roofline kernel(s)
 
+    def roof_kernels(self, mode: str) -> tuple[str, ...]:
+        """Kernels whose summed duration per step is the roofline launch."""
+        raise NotImplementedError
+
+    def roof_footprint(self):
+        """Device tensor streamed to measure the Infinity-Cache peak of a warm run."""
+        return None
+
+
+class GemvF32(Workload):
     """configs[0]: fp32 y = A.x, A 4096x4096 and x from U[-1,1) (seed 4242)."""
-    name = "gemv_f32_4096x4096"
     unit = "GB/s"
     dtype = "f32"
-    dominant = "gemv_f32"
+    ic_resident = True
 
     def __init__(self, M=4096, K=4096):
         import numpy as np
         import torch
         from l2domain_amd import gen
-        self.M, self.K = M, K
         from l2domain_amd.domain import home_map
         from l2domain_amd.gemv import workspace as gemv_workspace
+        self.M, self.K = M, K
+        self.name = f"gemv_f32_{M}x{K}"
         A, x = gen.gemv_f32_inputs(M, K)
         self.hA, self.hx = A, x
         self.A = torch.from_numpy(A).cuda()
@@ -63,6 +112,7 @@ class GemvF32:
         self.home = home_map(self.A)
         self.ws = gemv_workspace(M, K, self.A.dtype)
         self.bytes = 4 * M * K + 4 * K + 4 * M
+        self.roof_bytes = self.bytes
         self.np = np
 
     def step(self, mode):
@@ -72,62 +122,48 @@ class GemvF32:
     def throughput(self, sec_per_step):
         return self.bytes / sec_per_step / 1e9
 
+    def tol(self):
+        return 1e-3
+
     def verify(self):
         import oracle as ora
-        ref, yabs = ora.gemv_f64(self.hA, self.hx, nthreads=_cpu_threads())
+        ref, _ = ora.gemv_f64(self.hA, self.hx, nthreads=cpu_threads())
         ok = True
         for mode in MODES:
             self.step(mode)
             y = self.y.cpu().numpy()
             rel = float(self.np.max(self.np.abs(y - ref)) / self.np.max(self.np.abs(ref)))
-            ok = ok and rel <= 1e-3
+            ok = ok and rel <= self.tol()
         return ok
 
-    def roofline(self, sec_per_launch):
-        achieved = self.bytes / sec_per_launch / 1e9
-        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": self.kernel_name(), "algorithmic_bytes_per_launch": self.bytes}
+    def roof_kernels(self, mode):
+        return ("gemv_kernel", "gemv_exact_kernel", "gemv_rowhome_kernel", "gemv_seghome_kernel",
+                "gemv_chunkhome_kernel", "gemv_pieces_kernel")
 
-    def kernel_name(self):
-        # the aware launch routes rows by home die when a row divides an 8 KiB interleave chunk
-        row_bytes = self.A.element_size() * self.K
-        f16 = "true" if self.A.element_size() == 2 else "false"
-        if 8192 % row_bytes == 0:
-            return f"gemv_rowhome_kernel<{f16},*>"
-        if self.ws is not None and self.A.data_ptr() % 8192 == 0:
-            return f"gemv_seghome_kernel<{f16}>"
-        return f"gemv_exact_kernel<{f16},*>"
+    def roof_footprint(self):
+        return self.A
 
     def config(self):
         return {"workload": self.name, "M": self.M, "K": self.K, "dtype": "fp32", "seed": 4242}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, nt, budget_s):
         import oracle as ora
-        nt = _cpu_threads()
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 2.0:
-            ora.gemv_f32_seq(self.hA, self.hx, nthreads=nt)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(self.bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
-                "sample": f"{reps} full 4096x4096 fp32 GEMVs (oracle fp32 row loop, GEMV.cu:383-390)"}
+        dt, reps = timed_loop(lambda: ora.gemv_f32_seq(self.hA, self.hx, nthreads=nt), budget_s)
+        return self.bytes / dt / 1e9, f"{reps} x {self.M}x{self.K} fp32 GEMV (oracle fp32 row loop, GEMV.cu:383-390)"
 
 
 class GemvF16(GemvF32):
     """fp16 W (N(0,0.02), seed 4243), x (N(0,1), seed 4244), fp32 accumulate."""
     dtype = "f16->f32"
-    dominant = "gemv_f16f32"
 
     def __init__(self, M=14336, K=4096):
         import numpy as np
         import torch
         from l2domain_amd import gen
-        self.M, self.K = M, K
-        self.name = f"gemv_f16_{M}x{K}"
         from l2domain_amd.domain import home_map
         from l2domain_amd.gemv import workspace as gemv_workspace
+        self.M, self.K = M, K
+        self.name = f"gemv_f16_{M}x{K}"
         W, x = gen.gemv_f16_inputs(M, K)
         self.hA, self.hx = W, x
         self.A = torch.from_numpy(W).cuda()
@@ -136,41 +172,27 @@ class GemvF16(GemvF32):
         self.home = home_map(self.A)
         self.ws = gemv_workspace(M, K, self.A.dtype)
         self.bytes = 2 * M * K + 2 * K + 4 * M
+        self.roof_bytes = self.bytes
         self.np = np
 
-    def verify(self):
-        import oracle as ora
-        ref, _ = ora.gemv_f64(self.hA, self.hx, nthreads=_cpu_threads())
-        ok = True
-        for mode in MODES:
-            self.step(mode)
-            y = self.y.cpu().numpy()
-            ok = ok and float(self.np.max(self.np.abs(y - ref)) / self.np.max(self.np.abs(ref))) <= 2e-2
-        return ok
+    def tol(self):
+        return 2e-2
 
     def config(self):
         return {"workload": self.name, "M": self.M, "K": self.K, "dtype": "fp16 in, fp32 accumulate",
                 "seeds": [4243, 4244]}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, nt, budget_s):
         import oracle as ora
-        nt = _cpu_threads()
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 2.0:
-            ora.gemv_f64(self.hA, self.hx, nthreads=nt)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(self.bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
-                "sample": f"{reps} full {self.M}x{self.K} fp16 GEMVs (oracle row loop)"}
+        dt, reps = timed_loop(lambda: ora.gemv_f64(self.hA, self.hx, nthreads=nt), budget_s)
+        return self.bytes / dt / 1e9, f"{reps} x {self.M}x{self.K} fp16 GEMV (oracle row loop)"
 
 
-class Hist:
+class Hist(Workload):
     """2^28 u32 keys ~ Zipf(1.1) over 2^20 bins (seed 1373), bit-exact counts."""
     name = "hist_2p28_zipf1.1_2p20bins"
     unit = "Gkeys/s"
     dtype = "u32"
-    dominant = "hist_partition"
 
     def __init__(self, n=1 << 28, num_bins=1 << 20):
         import torch
@@ -185,6 +207,7 @@ class Hist:
         torch.cuda.synchronize()
         # algorithmic bytes: 4 B per key read + 4 B per counter written
         self.bytes = 4 * n + 4 * num_bins
+        self.roof_bytes = 4 * n  # the partition pass reads every key once
 
     def step(self, mode):
         self.h(self.keys, self.counts, mode=mode, home_attr=self.home)
@@ -196,7 +219,7 @@ class Hist:
         import numpy as np
         import oracle as ora
         host = self.keys.cpu().numpy().view(np.uint32)
-        ref, _ = ora.histogram(host, self.num_bins, nthreads=_cpu_threads())
+        ref, _ = ora.histogram(host, self.num_bins, nthreads=cpu_threads())
         self._host = host
         ok = True
         for mode in MODES:
@@ -205,49 +228,28 @@ class Hist:
             ok = ok and bool(np.array_equal(got, ref))
         return ok
 
-    def roofline(self, sec_per_launch):
-        # dominant kernel: the partition pass; its algorithmic traffic is the 4 B/key read.
-        # traffic: rocprofv3 --pmc FETCH_SIZE (x2.000, copy-kernel calibration) + WRITE_SIZE of
-        # the aware (routed) launch at this configuration: 1,073,954,202 B read + 540,019,405 B
-        # written.
-        achieved = 4 * self.n / sec_per_launch / 1e9
-        traffic = 1613854300 if (self.n, self.num_bins) == (1 << 28, 1 << 20) else None
-        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "hist_partition_kernel",
-                "algorithmic_bytes_per_launch": 4 * self.n}
-
-    def op_roofline(self, sec_per_step):
-        achieved = self.bytes / sec_per_step / 1e9
-        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": self.bytes}
+    def roof_kernels(self, mode):
+        return ("hist_partition_kernel",)
 
     def config(self):
         return {"workload": self.name, "keys": self.n, "bins": self.num_bins, "zipf_s": 1.1, "seed": 1373,
                 "bin_map": "scrambled rank ((r+1)*0x9E3779B1 mod 2^20)"}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, nt, budget_s):
         import numpy as np
         import oracle as ora
-        nt = _cpu_threads()
         sample = self._host[: 1 << 26] if hasattr(self, "_host") else self.keys[: 1 << 26].cpu().numpy().view(np.uint32)
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 10.0:
-            ora.histogram(sample, self.num_bins, nthreads=nt)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(sample.size / dt / 1e9, 4), "unit": "Gkeys/s", "cores": nt, "kind": "port",
-                "sample": f"{reps} x 2^26 keys of the same Zipf stream (oracle counting loop, HIST.cu:279-288, "
-                          f"{nt} threads with private histograms)"}
+        dt, reps = timed_loop(lambda: ora.histogram(sample, self.num_bins, nthreads=nt), budget_s)
+        return sample.size / dt / 1e9, (f"{reps} x 2^26 keys of the same Zipf stream (oracle counting loop, "
+                                         f"HIST.cu:279-288; threads keep private histograms)")
 
 
-class Hash:
+class Hash(Workload):
     """2^26 distinct u64 keys + values inserted at load factor 0.5 (2^27 slots),
     then 2^26 lookups at 50% hits. A step = clear + insert + lookup."""
     name = "hash_2p26_lf0.5_u64"
     unit = "Mops/s"
     dtype = "u64"
-    dominant = "hash_lookup"
 
     def __init__(self):
         import torch
@@ -259,6 +261,8 @@ class Hash:
         self.v = torch.empty(self.n, dtype=torch.int64, device="cuda")
         self.f = torch.empty(self.n, dtype=torch.uint8, device="cuda")
         torch.cuda.synchronize()
+        # insert: 16 B key/value in + one 16 B slot written per key
+        self.roof_bytes = 32 * self.n
 
     def step(self, mode):
         self.t.clear()
@@ -276,8 +280,9 @@ class Hash:
         hq = self.q.cpu().numpy().view(np.uint64)
         ref = ora.HashTable(self.slots)
         ref.build(hk, hv)
-        rv, rf = ref.lookup(hq, nthreads=_cpu_threads())
+        rv, rf = ref.lookup(hq, nthreads=cpu_threads())
         self._ref = (hk, hv, hq)
+        del ref
         ok = True
         for mode in MODES:
             self.step(mode)
@@ -286,39 +291,35 @@ class Hash:
             ok = ok and bool(np.array_equal(self.v.cpu().numpy().view(np.uint64), rv))
         return ok
 
-    def roofline(self, sec_per_launch):
-        # algorithmic bytes: lookup = 8 B key + 16 B slot + 8 B value + 1 B found per query
-        achieved = 33 * self.n / sec_per_launch / 1e9
-        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "hash_lookup_kernel",
-                "algorithmic_bytes_per_launch": 33 * self.n}
+    def roof_kernels(self, mode):
+        return ("hash_insert_kernel",)
 
     def config(self):
         return {"workload": self.name, "keys": self.n, "slots": self.slots, "lookups": self.n, "hit_rate": 0.5,
                 "seed": 42}
 
-    def cpu_baseline(self):
-        import numpy as np
+    def cpu_baseline(self, nt, budget_s):
         import oracle as ora
         hk, hv, hq = self._ref
-        m = 1 << 23
         t0 = time.perf_counter()
-        ref = ora.HashTable(1 << 24)
-        ref.build(hk[:m], hv[:m])
-        ref.lookup(hq[:m], nthreads=1)
-        dt = time.perf_counter() - t0
-        return {"value": round(2 * m / dt / 1e6, 3), "unit": "Mops/s", "cores": 1, "kind": "port",
-                "sample": "2^23 serial inserts into 2^24 slots + 2^23 lookups (oracle, HASH.cu:46-64,226-241)"}
+        ref = ora.HashTable(self.slots)
+        ref.build(hk, hv)
+        t1 = time.perf_counter()
+        ref.lookup(hq, nthreads=nt)
+        t2 = time.perf_counter()
+        del ref
+        return 2 * self.n / (t2 - t0) / 1e6, (f"the whole config once: 2^26 serial inserts into 2^27 slots "
+                                               f"({t1 - t0:.2f} s, HASH.cu:226-241) + 2^26 lookups ({t2 - t1:.2f} s, "
+                                               f"HASH.cu:46-64)")
 
 
-class Hist256:
+class Hist256(Workload):
     """The reference's own histogram workload (histogram256_sideaware.cu): data_mb = 512 (the
     paper preset's largest, applications/histogram/run.sh:16) of words[i] = mix32(i), every
     byte counted into 256 bins. A step = one xd_hist256_u32bytes call (count + fused merge)."""
     name = "hist256_bytes_512MiB_mix32"
     unit = "GB/s"
     dtype = "u8"
-    dominant = "hist256"
     single_kernel = True
 
     def __init__(self, data_mb=512):
@@ -335,6 +336,7 @@ class Hist256:
         self.bh = ByteHistogram()
         self.counts = torch.empty(256, dtype=torch.int32, device="cuda")
         self.bytes = 4 * self.n + 4 * 256
+        self.roof_bytes = self.bytes
 
     def step(self, mode):
         self.bh(self.words, self.counts, mode=mode, home_attr=self.home)
@@ -345,42 +347,29 @@ class Hist256:
     def verify(self):
         import numpy as np
         import oracle as ora
-        ref = ora.hist256_bytes(self.host, nthreads=_cpu_threads())
+        ref = ora.hist256_bytes(self.host, nthreads=cpu_threads())
         ok = True
         for mode in MODES:
             self.step(mode)
             ok = ok and bool(np.array_equal(self.counts.cpu().numpy().view(np.uint32), ref))
         return ok
 
-    def roofline(self, sec_per_launch):
-        achieved = self.bytes / sec_per_launch / 1e9
-        # traffic: rocprofv3 --pmc FETCH_SIZE (x2.000, copy-kernel calibration) + WRITE_SIZE of
-        # this kernel at this configuration: 537,088,000 B read + 550,912 B written.
-        traffic = 537638912 if self.data_mb == 512 else None
-        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": "hist256_kernel",
-                "algorithmic_bytes_per_launch": self.bytes}
+    def roof_kernels(self, mode):
+        return ("hist256_kernel",)
 
     def config(self):
         return {"workload": self.name, "data_mb": self.data_mb, "words": self.n, "bins": 256,
                 "data": "words[i] = mix32(i) (HIST.cu:331-340)"}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, nt, budget_s):
         import oracle as ora
-        nt = _cpu_threads()
         sample = self.host[: 1 << 26]
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 5.0:
-            ora.hist256_bytes(sample, nthreads=nt)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(4 * sample.size / dt / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
-                "sample": f"{reps} x 2^26 words of the same data (oracle byte-counting loop, HIST.cu:279-288, "
-                          f"{nt} threads with private histograms)"}
+        dt, reps = timed_loop(lambda: ora.hist256_bytes(sample, nthreads=nt), budget_s)
+        return 4 * sample.size / dt / 1e9, (f"{reps} x 2^26 words of the same data (oracle byte-counting loop, "
+                                             f"HIST.cu:279-288)")
 
 
-class BfsRef:
+class BfsRef(Workload):
     """The reference's own BFS workload at its paper preset (applications/bfs/run.sh:24-27):
     2,000,000 vertices of degree 64 in its directed hot-pool graph (hot_per_side 200,000,
     dst_local 95 %, seed 8201; sides from the measured homes of this run's buffers), 4096
@@ -388,7 +377,7 @@ class BfsRef:
     name = "bfs_ref_V2M_deg64_src4096_depth4"
     unit = "GTEPS"
     dtype = "int32"
-    dominant = "bfs_multi"
+    cpu_parallel = False
 
     def __init__(self):
         import numpy as np
@@ -402,6 +391,9 @@ class BfsRef:
         expanded = (self.ref != 0xFFFFFFFF) & (self.ref < self.depth)
         self.edges = int(np.diff(self.g.h_rowptr.astype(np.int64))[expanded].sum())
         self.nexp = int(expanded.sum())
+        # adjacency lists of the expanded vertices, their two rowptr entries, and the level
+        # array written once (initialisation)
+        self.roof_bytes = 4 * self.edges + 8 * self.nexp + 4 * self.V
         self.np = np
 
     def step(self, mode):
@@ -418,33 +410,22 @@ class BfsRef:
             ok = ok and bool(self.np.array_equal(got, self.ref))
         return ok
 
-    def roofline(self, sec_per_launch):
-        # adjacency lists of the expanded vertices, their two rowptr entries, and the level
-        # array written once (initialisation)
-        nbytes = 4 * self.edges + 8 * self.nexp + 4 * self.V
-        achieved = nbytes / sec_per_launch / 1e9
-        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "bfs search (multi_init/seed/level kernels)", "algorithmic_bytes_per_bfs": nbytes}
+    def roof_kernels(self, mode):
+        return ("multi_init_kernel", "multi_seed_kernel", "multi_level_kernel")
 
     def config(self):
         return {"workload": self.name, "vertices": self.V, "degree": self.deg, "sources": self.nsrc,
                 "depth": self.depth, "dst_local_pct": self.dl, "hot_per_side": self.H, "seed": 8201,
                 "edges_walked": self.edges, "reached": self.reached}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, nt, budget_s):
         import oracle as ora
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 5.0:
-            ora.bfs_multi(self.g.h_rowptr, self.g.h_col, self.g.h_sources, self.depth)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(self.edges / dt / 1e9, 4), "unit": "GTEPS", "cores": 1, "kind": "port",
-                "sample": f"{reps} full serial multi-source searches of the same graph (oracle, bfs.cu:215-252)"}
+        dt, reps = timed_loop(lambda: ora.bfs_multi(self.g.h_rowptr, self.g.h_col, self.g.h_sources, self.depth),
+                              budget_s)
+        return self.edges / dt / 1e9, f"{reps} serial multi-source searches of the same graph (oracle, BFS.cu:215-252)"
 
 
-class HashDep:
+class HashDep(Workload):
     """The reference's own hash workload (hash_probe_dep.cu, defaults :124-130): K = 32000000
     int32 keys with successors in 2^26 8-byte entries, two hot pools of 100000 keys homed on
     opposite I/O dies, 8000000 queries (80 % hot) following their chains for 4 dependent
@@ -452,8 +433,8 @@ class HashDep:
     name = "hash_dep_K32M_Q8M_C2p26_L4"
     unit = "Mprobes/s"
     dtype = "int32"
-    dominant = "dep_probe"
     single_kernel = True
+    cpu_parallel = False
 
     def __init__(self, K=32000000, Q=8000000, slots=1 << 26, L=4, hot=80, H=100000):
         import torch
@@ -465,6 +446,8 @@ class HashDep:
         self.build_s = time.perf_counter() - t0
         self.q = torch.from_numpy(self.hq).cuda()
         self.out = torch.empty(Q, dtype=torch.int32, device="cuda")
+        # latency-bound dependent chains: 8 B entry per probe + 4 B query in + 4 B out
+        self.roof_bytes = 8 * Q * L + 8 * Q
 
     def step(self, mode):
         self.t.probe(self.q, self.L, mode=mode, out=self.out)
@@ -482,40 +465,27 @@ class HashDep:
             ok = ok and bool(np.array_equal(self.out.cpu().numpy(), ref))
         return ok
 
-    def roofline(self, sec_per_launch):
-        # latency-bound dependent chains: algorithmic bytes = 8 B entry per probe + 4 B query
-        # in + 4 B out per query
-        nbytes = 8 * self.Q * self.L + 8 * self.Q
-        achieved = nbytes / sec_per_launch / 1e9
-        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "dep_probe_kernel",
-                "algorithmic_bytes_per_launch": nbytes}
+    def roof_kernels(self, mode):
+        return ("dep_probe_kernel",)
 
     def config(self):
         return {"workload": self.name, "K": self.K, "Q": self.Q, "C": self.slots, "L": self.L, "hot_pct": self.hot,
                 "H": self.H, "seed": 42, "host_build_s": round(self.build_s, 2)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, nt, budget_s):
         import oracle as ora
         n = 1 << 20
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 5.0:
-            ora.dep_probe(self.t.host_table, self.slots, self.hq[:n], self.L)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(n * self.L / dt / 1e6, 3), "unit": "Mprobes/s", "cores": 1, "kind": "port",
-                "sample": f"{reps} x 2^20 queries of the same stream (oracle probe_dep_base loop, HASH.cu:66-83)"}
+        dt, reps = timed_loop(lambda: ora.dep_probe(self.t.host_table, self.slots, self.hq[:n], self.L), budget_s)
+        return n * self.L / dt / 1e6, f"{reps} x 2^20 queries of the same stream (oracle probe_dep_base loop, HASH.cu:66-83)"
 
 
-class Bfs:
+class Bfs(Workload):
     """undirected R-MAT scale 22, edge factor 16, a/b/c/d = .57/.19/.19/.05 (seed
     8201), CSR int32, source 0. A step = one BFS to completion."""
     name = "bfs_rmat22_ef16"
     unit = "GTEPS"
     dtype = "int32"
-    dominant = "bfs_level"
-    single_kernel = True  # roofline over the whole search (init, levels, control, conversion)
+    cpu_parallel = False
 
     def __init__(self):
         from l2domain_amd.bfs import RMAT_EDGE_FACTOR, RMAT_SCALE, RMAT_SEED, Graph, rmat_csr
@@ -524,6 +494,10 @@ class Bfs:
         self.gen_s = time.perf_counter() - t0
         self.g = Graph(self.rowptr, self.col)
         self.stats = None
+        self.step("aware")
+        V = self.g.V
+        # CSR read once + level written once per search: 4(V+1) + 4 nnz_reached + 4V
+        self.roof_bytes = 4 * (V + 1) + 4 * self.stats["reached_edges"] + 4 * V
 
     def step(self, mode):
         _, self.stats = self.g.bfs(0, mode=mode)
@@ -541,15 +515,8 @@ class Bfs:
             ok = ok and bool(np.array_equal(self.g.level.cpu().numpy().view(np.uint32), ref))
         return ok
 
-    def roofline(self, sec_per_launch):
-        # algorithmic bytes per search: CSR read once + level written once, 4(V+1) + 4 nnz + 4V,
-        # over the time of the whole search (sec_per_launch is the per-step time here)
-        V = self.g.V
-        nbytes = 4 * (V + 1) + 4 * self.stats["reached_edges"] + 4 * V
-        achieved = nbytes / sec_per_launch / 1e9
-        return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "bfs search (bfs_level/hubs/control/b2q kernels)", "algorithmic_bytes_per_bfs": nbytes}
+    def roof_kernels(self, mode):
+        return ("bfs_init_kernel", "bfs_level_kernel", "bfs_hubs_kernel", "bfs_control_kernel")
 
     def config(self):
         return {"workload": self.name, "vertices": self.g.V, "nnz": self.g.nnz, "source": 0, "seed": 8201,
@@ -557,16 +524,10 @@ class Bfs:
                 "reached_edges": self.stats["reached_edges"] if self.stats else None,
                 "host_generation_s": round(self.gen_s, 2)}
 
-    def cpu_baseline(self):
+    def cpu_baseline(self, nt, budget_s):
         import oracle as ora
-        t0 = time.perf_counter()
-        reps = 0
-        while time.perf_counter() - t0 < 3.0:
-            ora.bfs(self.rowptr, self.col, 0)
-            reps += 1
-        dt = (time.perf_counter() - t0) / reps
-        return {"value": round(self.stats["reached_edges"] / 2 / dt / 1e9, 4), "unit": "GTEPS", "cores": 1,
-                "kind": "port", "sample": f"{reps} full serial queue BFS runs of the same graph (oracle)"}
+        dt, reps = timed_loop(lambda: ora.bfs(self.rowptr, self.col, 0), budget_s)
+        return self.stats["reached_edges"] / 2 / dt / 1e9, f"{reps} serial queue BFS runs of the same graph (oracle)"
 
 
 WORKLOADS = {
@@ -581,20 +542,23 @@ WORKLOADS = {
     "gemv_f16_down": lambda: GemvF16(4096, 14336),
 }
 DEFAULT_WORKLOAD = "hist"
-# every other BASELINE config, reported under "extras" of the same JSON line
+# every other configuration, reported under "configs" of the same JSON line: (name, cold)
 EXTRAS = (("gemv_f32", False), ("gemv_f32", True), ("gemv_f16_up", False), ("gemv_f16_up", True),
-          ("gemv_f16_down", False), ("gemv_f16_down", True), ("hash", False), ("hash_dep", False),
-          ("bfs", False), ("hist256", True), ("hist256", False), ("bfs_ref", False))
+          ("gemv_f16_down", False), ("gemv_f16_down", True), ("hash", False), ("bfs", False),
+          ("hash_dep", False), ("hist256", True), ("hist256", False), ("bfs_ref", False))
 
 
 # ---------------------------------------------------------------------------------------
 # Timing
 # ---------------------------------------------------------------------------------------
 def time_steps(wl, mode, steps, warmup, flusher=None):
-    """Returns seconds per step over exactly `steps` steps (HIP events on the launch stream)."""
+    """Seconds per step over exactly `steps` steps, HIP events on the launch stream. Cold:
+    a flush before every step, each step timed by its own event pair."""
     import torch
     stream = torch.cuda.current_stream()
     for _ in range(warmup):
+        if flusher is not None:
+            flusher.flush()
         wl.step(mode)
     torch.cuda.synchronize()
     if flusher is None:
@@ -606,7 +570,6 @@ def time_steps(wl, mode, steps, warmup, flusher=None):
         e1.record(stream)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / 1e3 / steps
-    # cold: flush before each step, time each step separately
     total = 0.0
     for _ in range(steps):
         flusher.flush()
@@ -621,7 +584,7 @@ def time_steps(wl, mode, steps, warmup, flusher=None):
 
 
 def kernel_times(wl, mode, steps, flusher=None):
-    """Per-kernel average launch duration (s) from the library's HIP events, over `steps` steps."""
+    """{kernel: (seconds per step, launches per step)} from the dispatch-stamped events."""
     import torch
     from l2domain_amd import _lib
     torch.cuda.synchronize()
@@ -633,41 +596,119 @@ def kernel_times(wl, mode, steps, flusher=None):
     torch.cuda.synchronize()
     t = _lib.timing_read()
     _lib.timing_enable(False)
-    return {k: (ms / 1e3 / max(n, 1), n) for k, (ms, n) in t.items()}
+    t.pop("cache_flush_kernel", None)
+    return {k: (ms / 1e3 / steps, n / steps) for k, (ms, n) in t.items()}
 
 
-def launch_seconds(wl, r):
-    """Average duration of the dominant kernel in the aware mode. A one-kernel step is timed by
-    the back-to-back timed region (per-launch events would add their own overhead to a ~10 us
-    kernel); otherwise by the library's HIP events around that kernel."""
-    if getattr(wl, "single_kernel", False):
-        return r["sec"]["aware"]
-    return r["kernels"][wl.dominant][0]
+def ic_peak(wl, steps):
+    """Best warm read-stream throughput (GB/s) over the workload's own footprint, after one
+    untimed pass: a sweep of chunk order (aware, oblivious), workgroups and loads in flight.
+    The Infinity-Cache roofline of a warm run of that footprint."""
+    import torch
+    from l2domain_amd.domain import home_map, read_stream
+    buf = wl.roof_footprint()
+    home = getattr(wl, "home", None)
+    if home is None:
+        home = home_map(buf.view(torch.uint8))
+    nbytes = buf.numel() * buf.element_size()
+    res = {}
+    stream = torch.cuda.current_stream()
+    for mode in ("oblivious", "aware"):
+        for wgs in (1024, 2048, 4096):
+            for depth in (2, 4, 8):
+                read_stream(buf, mode, home, wgs, depth)
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(steps):
+                    read_stream(buf, mode, home, wgs, depth)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                res[f"{mode}/{wgs}/{depth}"] = nbytes / (e0.elapsed_time(e1) / 1e3 / steps) / 1e9
+    best = max(res, key=res.get)
+    return res[best], {"best": best, **{k: round(v, 1) for k, v in res.items()}}
 
 
-def run_workload(name, steps, warmup, cold=False, with_cpu=True):
+def run_workload(name, steps, warmup, cold=False, modes=MODES, cpu=True, cpu_budget=2.0):
     import torch
     from l2domain_amd.domain import CacheFlusher
     wl = WORKLOADS[name]()
     ok = wl.verify()
     flusher = CacheFlusher() if cold else None
-    res = {}
-    for mode in MODES:
-        res[mode] = time_steps(wl, mode, steps, warmup, flusher)
+    sec = {m: time_steps(wl, m, steps, warmup, flusher) for m in modes}
     torch.cuda.synchronize()
-    kt = kernel_times(wl, "aware", steps, flusher)
-    kt_modes = {m: (kt if m == "aware" else kernel_times(wl, m, min(steps, 5), flusher)) for m in MODES}
-    out = {
-        "workload": wl,
-        "verified": ok,
-        "sec": res,
-        "tput": {m: wl.throughput(s) for m, s in res.items()},
-        "kernels": kt,
-        "kernels_by_mode": kt_modes,
-    }
-    if with_cpu:
-        out["cpu"] = wl.cpu_baseline()
+    kt = {m: kernel_times(wl, m, steps, flusher) for m in modes}
+    roof_s = {m: sum(v[0] for k, v in kt[m].items() if k in wl.roof_kernels(m)) for m in modes}
+    step_kernel_s = {m: sum(v[0] for v in kt[m].values()) for m in modes}
+    # cold steps: the kernels' own durations (the flush and the dispatch gaps are not the step)
+    tput_s = step_kernel_s if cold else sec
+    out = {"workload": wl, "verified": ok, "sec": sec, "tput_s": tput_s, "roof_s": roof_s, "kernels": kt,
+           "tput": {m: wl.throughput(tput_s[m]) for m in modes}}
+    if not cold and wl.ic_resident:
+        out["ic_peak"] = ic_peak(wl, steps)
+    if cpu:
+        nt = cpu_threads()
+        v1, s1 = wl.cpu_baseline(1, cpu_budget)
+        cb = {"value_1thread": round(v1, 4), "sample": s1, "kind": "port"}
+        if wl.cpu_parallel and nt > 1:
+            vn, _ = wl.cpu_baseline(nt, cpu_budget)
+            cb.update(value=round(vn, 4), cores=nt)
+        else:
+            cb.update(value=round(v1, 4), cores=1)
+        cb["unit"] = wl.unit
+        out["cpu"] = cb
     return out
+
+
+def roofline(r, mode="aware", cold=False):
+    wl = r["workload"]
+    sec = r["roof_s"][mode]
+    achieved = wl.roof_bytes / sec / 1e9 if sec > 0 else 0.0
+    if "ic_peak" in r:
+        bound, peak = "infinity_cache", r["ic_peak"][0]
+    else:
+        bound, peak = "hbm", HBM_PEAK_GBS
+    name = getattr(wl, "name", "")
+    traffic = TRAFFIC.get((name, "cold" if cold else "warm", mode))
+    return {"bound": bound, "achieved": round(achieved, 1), "peak": round(peak, 1), "unit": "GB/s",
+            "frac": round(achieved / peak, 4), "traffic": traffic,
+            "kernel": "+".join(k for k in r["kernels"][mode] if k in wl.roof_kernels(mode)),
+            "kernel_us": round(sec * 1e6, 3), "bytes": wl.roof_bytes}
+
+
+def compact(r, cold):
+    """One short entry per configuration (the driver keeps only the tail of the line)."""
+    t = r["tput"]
+    e = {"ok": r["verified"], "unit": r["workload"].unit}
+    for m, k in (("aware", "aware"), ("oblivious", "obl"), ("rotated", "rot")):
+        if m in t:
+            e[k] = round(t[m], 2)
+    if "oblivious" in t and "aware" in t:
+        e["sp"] = round(r["tput_s"]["oblivious"] / r["tput_s"]["aware"], 4)
+    if "oblivious" in t and "rotated" in t:
+        e["sp_rot"] = round(r["tput_s"]["oblivious"] / r["tput_s"]["rotated"], 4)
+    if "aware" in t:
+        ro = roofline(r, "aware", cold)
+        e["roof"] = {k: ro[k] for k in ("bound", "achieved", "peak", "frac", "traffic", "kernel_us")}
+    if "cpu" in r:
+        c = r["cpu"]
+        e["cpu"] = {"v": c["value"], "v1": c["value_1thread"], "cores": c["cores"]}
+    return e
+
+
+def detail(r, cold):
+    d = {"verified": r["verified"], "cache": "cold" if cold else "warm", "config": r["workload"].config(),
+         "ms_per_step_events": {m: round(s * 1e3, 6) for m, s in r["sec"].items()},
+         "ms_per_step_kernels": {m: round(sum(v[0] for v in kk.values()) * 1e3, 6) for m, kk in r["kernels"].items()},
+         "kernels_us_per_step": {m: {k: [round(v[0] * 1e6, 3), v[1]] for k, v in kk.items()}
+                                 for m, kk in r["kernels"].items()},
+         "roofline_by_mode": {m: roofline(r, m, cold) for m in r["kernels"]}}
+    if "ic_peak" in r:
+        d["ic_peak_gbs"] = r["ic_peak"][1]
+    if "cpu" in r:
+        d["cpu_baseline"] = r["cpu"]
+    return d
 
 
 def main():
@@ -677,14 +718,20 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
     ap.add_argument("--cold", action="store_true", help="flush L2 + Infinity Cache before every step")
-    ap.add_argument("--only", action="store_true", help="measure the selected workload only (no extras)")
+    ap.add_argument("--only", action="store_true", help="measure the selected workload only (no other configs)")
+    ap.add_argument("--modes", default=",".join(MODES), help="comma list of modes to time (default: all three)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--detail", default=None, help="write per-kernel, per-mode detail to this JSON file")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py: this build measures one MI355X only (one-GPU tier); "
               f"--gpus {args.gpus} / WORLD_SIZE={world} is not supported", file=sys.stderr)
+        sys.exit(2)
+    modes = tuple(m for m in MODES if m in args.modes.split(","))
+    if not modes:
+        print("bench.py: --modes names none of oblivious, aware, rotated", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -693,12 +740,14 @@ def main():
         sys.exit(1)
     from l2domain_amd.domain import topology
 
-    r = run_workload(args.workload, args.steps, args.warmup, cold=args.cold, with_cpu=not args.no_cpu)
+    r = run_workload(args.workload, args.steps, args.warmup, cold=args.cold, modes=modes, cpu=not args.no_cpu,
+                     cpu_budget=10.0)
     wl = r["workload"]
-    sec = r["sec"]["aware"]
+    head = "aware" if "aware" in modes else modes[0]
+    sec = r["tput_s"][head]
     line = {
         "metric": METRIC,
-        "value": round(r["tput"]["aware"], 3),
+        "value": round(r["tput"][head], 3),
         "unit": wl.unit,
         "n_gpus": 1,
         "steps": args.steps,
@@ -709,48 +758,37 @@ def main():
         "vs_baseline": None,
         "dtype": wl.dtype,
         "data": "synthetic (seeded generators, inputs resident in HBM)",
-        "config": dict(wl.config(), cache="cold" if args.cold else "warm", mode="xcd_aware"),
+        "config": dict(wl.config(), cache="cold" if args.cold else "warm", mode=head),
         "verified": r["verified"],
-        "modes": {m: {"ms_per_step": round(r["sec"][m] * 1e3, 6), "value": round(r["tput"][m], 3)}
-                  for m in MODES},
-        "speedup_aware_vs_oblivious": round(r["sec"]["oblivious"] / r["sec"]["aware"], 4),
-        "speedup_rotated_vs_oblivious": round(r["sec"]["oblivious"] / r["sec"]["rotated"], 4),
-        "roofline": wl.roofline(launch_seconds(wl, r)),
-        "kernels_us": {k: round(v[0] * 1e6, 3) for k, v in r["kernels"].items()},
-        "kernels_us_by_mode": {m: {k: round(v[0] * 1e6, 3) for k, v in kk.items()}
-                               for m, kk in r["kernels_by_mode"].items()},
-        "cpu_baseline": r.get("cpu"),
-        "device": topology(0)["name"],
     }
-    if hasattr(wl, "op_roofline"):
-        line["roofline_op"] = wl.op_roofline(sec)
+    if "oblivious" in modes and "aware" in modes:
+        line["speedup_aware_vs_oblivious"] = round(r["tput_s"]["oblivious"] / r["tput_s"]["aware"], 4)
+    if "oblivious" in modes and "rotated" in modes:
+        line["speedup_rotated_vs_oblivious"] = round(r["tput_s"]["oblivious"] / r["tput_s"]["rotated"], 4)
+    line["modes"] = {m: round(v, 3) for m, v in r["tput"].items()}
+    line["roofline"] = roofline(r, head, args.cold)
+    line["cpu_baseline"] = r.get("cpu")
+    details = {f"{args.workload}_{'cold' if args.cold else 'warm'}": detail(r, args.cold)}
     if not args.only:
-        extras = {}
+        configs = {}
         esteps = min(args.steps, 50)
         for name, cold in EXTRAS:
             if name == args.workload and cold == args.cold:
                 continue
-            print(f"bench.py: extra {name} ({'cold' if cold else 'warm'})", file=sys.stderr, flush=True)
-            e = run_workload(name, esteps, min(args.warmup, 5), cold=cold, with_cpu=not args.no_cpu and not cold)
-            ew = e["workload"]
-            entry = {"verified": e["verified"], "unit": ew.unit, "steps": esteps,
-                     "cache": "cold" if cold else "warm", "config": ew.config(),
-                     "value_aware": round(e["tput"]["aware"], 3),
-                     "value_oblivious": round(e["tput"]["oblivious"], 3),
-                     "value_rotated": round(e["tput"]["rotated"], 3),
-                     "speedup_aware_vs_oblivious": round(e["sec"]["oblivious"] / e["sec"]["aware"], 4),
-                     "speedup_rotated_vs_oblivious": round(e["sec"]["oblivious"] / e["sec"]["rotated"], 4),
-                     "roofline": ew.roofline(launch_seconds(ew, e)),
-                     "kernels_us": {k: round(v[0] * 1e6, 3) for k, v in e["kernels"].items()},
-                     "kernels_us_by_mode": {m: {k: round(v[0] * 1e6, 3) for k, v in kk.items()}
-                                            for m, kk in e["kernels_by_mode"].items()}}
-            if "cpu" in e:
-                entry["cpu_baseline"] = e["cpu"]
-            extras[f"{name}_{'cold' if cold else 'warm'}"] = entry
-            del e, ew
+            key = f"{name}_{'cold' if cold else 'warm'}"
+            print(f"bench: {key}", file=sys.stderr, flush=True)
+            e = run_workload(name, esteps, min(args.warmup, 5), cold=cold, modes=modes,
+                             cpu=not args.no_cpu and not cold)
+            configs[key] = compact(e, cold)
+            details[key] = detail(e, cold)
+            del e
             torch.cuda.empty_cache()
-        line["extras"] = extras
-    print(json.dumps(line), flush=True)
+        line["configs"] = configs
+    line["device"] = topology(0)["name"]
+    if args.detail:
+        Path(args.detail).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.detail).write_text(json.dumps(details, indent=1))
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":

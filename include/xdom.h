@@ -75,7 +75,9 @@ const char *xd_version(void);
 const char *xd_last_error(void);
 
 /* Per-kernel timing of the library's own launches, for benchmarks: when enabled, every
- * kernel launch is bracketed by HIP events on its launch stream. xd_timing_enable resets
+ * kernel dispatch stamps a start/stop HIP event pair itself (hipExtLaunchKernel), so a
+ * kernel's time is its own execution, without the gaps between dispatches; kernels are
+ * named after their __global__ functions. xd_timing_enable resets
  * the accumulators; xd_timing_query(i, ...) reports kernel number i (in first-launch order)
  * with its summed duration and launch count, waiting for outstanding launches; it returns
  * XD_ERR_INVALID_ARG past the last kernel. No counterpart in the reference (which times
@@ -153,6 +155,17 @@ size_t xd_cache_flush_bytes(void);
  * size the flush from cudaDeviceProp::l2CacheSize. */
 int xd_cache_flush(const void *buf, size_t bytes, void *stream);
 
+/* Read `bytes` of `buf` (device) once, 16 bytes per load, and discard the words: the
+ * roofline probe of cache-resident workloads (the warm GEMV configurations). Oblivious:
+ * contiguous; XD_MODE_AWARE: each I/O die reads only the 8 KiB chunks it homes (home_attr =
+ * xd_home_map() of buf, or NULL for the address-mask prediction; buf and bytes in whole
+ * 16 KiB pairs); XD_MODE_ROTATED: only the far chunks. Launch shape: `workgroups` (a
+ * multiple of 8; 0 = 2048) of 256 threads, each thread keeping 2 x `depth` (1, 2, 4 or 8;
+ * 0 = 4) loads in flight. No counterpart in the reference, whose warm runs (touch_k,
+ * histogram256_sideaware.cu:27-37) have no bandwidth ceiling. */
+int xd_read_stream(const void *buf, size_t bytes, int mode, const uint8_t *home_attr, int workgroups, int depth,
+                   void *stream);
+
 /* ------------------------------------------------------------------------------------ */
 /* GEMV  y[M] = A[M,K] . x[K], row-major A, fp32 accumulation                            */
 /* ------------------------------------------------------------------------------------ */
@@ -211,15 +224,17 @@ size_t xd_hist_workspace_size(size_t n, uint32_t num_bins);
  * generalised from 256 byte-bins (add_word, :20-25) to one bin per key. XD_MODE_AWARE
  * has each I/O die read only the 8 KiB key chunks it homes (as the reference's side-aware
  * chunks do; home_attr = xd_home_map() of the keys, device, optional: NULL = the
- * address-mask prediction) and range-partitions the bins over the XCDs: XCD x counts and
- * merges only its bin range. XD_MODE_ROTATED reads the far chunks and counts each range on
- * another XCD. */
+ * address-mask prediction) and range-partitions the bins over the XCDs for counting: XCD
+ * x counts only its bin range (the final merge runs over the whole grid in every mode).
+ * XD_MODE_ROTATED reads the far chunks and counts each range on another XCD. An error
+ * returned after the first kernel was enqueued (a HIP launch failure) leaves the workspace
+ * dirty: zero-fill it again before the next call. */
 int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_bins, int mode,
                 const uint8_t *home_attr, void *workspace, size_t workspace_bytes, void *stream);
 
-/* Workspace bytes of xd_hist256_u32bytes (independent of n; about 520 KB). Zero-filled once
- * when allocated; every call leaves its tickets zeroed again. Calls sharing one workspace
- * must not overlap. */
+/* Workspace bytes of xd_hist256_u32bytes (independent of n: 8448 bytes of accumulators and
+ * tickets). Zero-filled once when allocated; every call leaves it zeroed again. Calls
+ * sharing one workspace must not overlap. */
 size_t xd_hist256_workspace_size(void);
 
 /* The reference's own histogram: 256 byte-bins, every byte of every word counted,
@@ -232,6 +247,7 @@ size_t xd_hist256_workspace_size(void);
  * words, or NULL for the address-mask prediction); XD_MODE_ROTATED only the far chunks. */
 int xd_hist256_u32bytes(const uint32_t *words, size_t n, uint32_t *counts, int mode, const uint8_t *home_attr,
                         void *workspace, size_t workspace_bytes, void *stream);
+
 
 /* ------------------------------------------------------------------------------------ */
 /* Hash table: open addressing, linear probing, uint64 keys and values                   */

@@ -80,6 +80,7 @@ SIGNATURES: dict[str, tuple] = {
     "xd_home_map": (I, [VP, SZ, VP, VP, SZ, VP]),
     "xd_cache_flush_bytes": (SZ, []),
     "xd_cache_flush": (I, [VP, SZ, VP]),
+    "xd_read_stream": (I, [VP, SZ, I, VP, I, I, VP]),
     "xd_xdom_pchase": (I, [I, I, VP, SZ, I, I, VP, SZ, VP, VP]),
     "xd_mask_probe": (I, [VP, SZ, I, I, I, VP, VP]),
     "xd_gemv_workspace_size": (SZ, [I, I, I]),

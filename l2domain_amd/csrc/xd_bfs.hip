@@ -505,10 +505,10 @@ static int build_route(const int32_t *rowptr, const int32_t *col, int32_t V, int
     const int64_t nblocks = ((int64_t)V + 63) / 64;
     auto *bcount = static_cast<unsigned long long *>(route);
     auto *blist = reinterpret_cast<int32_t *>(static_cast<char *>(route) + kRouteHeader);
-    hipLaunchKernelGGL(bfs_clear2_kernel, dim3(1), dim3(64), 0, s, bcount);
+    launch("bfs_clear2_kernel", bfs_clear2_kernel, dim3(1), dim3(64), 0, s, bcount);
     if (nnz == 0) return launch_status("bfs_clear2_kernel");
     const HomeMap home{home_attr, reinterpret_cast<uint64_t>(col) / kHomePage, home_mask()};
-    hipLaunchKernelGGL(bfs_blocks_kernel, dim3((unsigned)((nblocks + kBlkThreads - 1) / kBlkThreads)), dim3(kBlkThreads),
+    launch("bfs_blocks_kernel", bfs_blocks_kernel, dim3((unsigned)((nblocks + kBlkThreads - 1) / kBlkThreads)), dim3(kBlkThreads),
                        0, s, rowptr, nblocks, reinterpret_cast<uint64_t>(col), nnz * (int64_t)sizeof(int32_t), home, blist,
                        bcount);
     return launch_status("bfs_blocks_kernel");
@@ -562,8 +562,7 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     const unsigned g256 = (unsigned)std::min<int64_t>(8192, ((int64_t)V + 255) / 256 + 1);
     const void *rt = route;
     {
-        KernelTimer kt("bfs_init", s);
-        hipLaunchKernelGGL(bfs_init_kernel, dim3(g256), dim3(256), 0, s, st, src, nnz);
+        launch("bfs_init_kernel", bfs_init_kernel, dim3(g256), dim3(256), 0, s, st, src, nnz);
         if (int rc = launch_status("bfs_init_kernel")) return rc;
         if (bmode != XD_MODE_OBLIVIOUS && rt == nullptr) {  // no prepared route: build one here
             if (int rc = build_route(rowptr, col, V, nnz, nullptr, ws + L.route, s)) return rc;
@@ -578,12 +577,11 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
         const int batch = enq == 0 ? kFirstBatch : kLevelBatch;
         for (int k = 0; k < batch; ++k, ++enq) {
             {
-                KernelTimer kt("bfs_level", s);
-                hipLaunchKernelGGL(bfs_level_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, st, bmode, blist, bcount,
+                launch("bfs_level_kernel", bfs_level_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, st, bmode, blist, bcount,
                                    L.nblocks);
             }
-            hipLaunchKernelGGL(bfs_hubs_kernel, dim3(kBigGrid), dim3(kBfsThreads), 0, s, st);
-            hipLaunchKernelGGL(bfs_control_kernel, dim3(1), dim3(kBfsThreads), 0, s, st, kBfsGrid);
+            launch("bfs_hubs_kernel", bfs_hubs_kernel, dim3(kBigGrid), dim3(kBfsThreads), 0, s, st);
+            launch("bfs_control_kernel", bfs_control_kernel, dim3(1), dim3(kBfsThreads), 0, s, st, kBfsGrid);
             if (int rc = launch_status("bfs level kernels")) return rc;
         }
         XD_HIP(hipMemcpyAsync(&h, st.ctl, sizeof(h), hipMemcpyDeviceToHost, s));

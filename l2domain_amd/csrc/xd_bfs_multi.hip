@@ -285,17 +285,16 @@ int xd_bfs_multi(const int32_t *rowptr, const int32_t *col, int32_t num_vertices
     int lg = 0;
     while (lg < 6 && (double)(2 << lg) <= mean * 1.5) ++lg;
 
-    KernelTimer kt("bfs_multi", s);
     const int igrid = (int)std::min<int64_t>(4096, ((int64_t)V + kMThreads - 1) / kMThreads);
-    hipLaunchKernelGGL(multi_init_kernel, dim3(std::max(igrid, 1)), dim3(kMThreads), 0, s, level, visited, counts, V);
+    launch("multi_init_kernel", multi_init_kernel, dim3(std::max(igrid, 1)), dim3(kMThreads), 0, s, level, visited, counts, V);
     if (int rc = launch_status("multi_init_kernel")) return rc;
     if (num_sources > 0) {
-        hipLaunchKernelGGL(multi_seed_kernel, dim3((num_sources + kMThreads - 1) / kMThreads), dim3(kMThreads), 0, s,
+        launch("multi_seed_kernel", multi_seed_kernel, dim3((num_sources + kMThreads - 1) / kMThreads), dim3(kMThreads), 0, s,
                            sources, num_sources, work_side, routed, level, visited, queues, counts, V);
         if (int rc = launch_status("multi_seed_kernel")) return rc;
     }
     for (int32_t d = 0; d < max_depth; ++d) {
-        hipLaunchKernelGGL(multi_level_kernel, dim3(kMGrid), dim3(kMThreads), 0, s, rowptr, col, work_side, level,
+        launch("multi_level_kernel", multi_level_kernel, dim3(kMGrid), dim3(kMThreads), 0, s, rowptr, col, work_side, level,
                            visited, queues, counts, V, (uint32_t)d, lg, mode, d % 3);
         if (int rc = launch_status("multi_level_kernel")) return rc;
     }

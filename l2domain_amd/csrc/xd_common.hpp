@@ -1,6 +1,7 @@
 // Shared device and host helpers of libxdom (gfx950 / CDNA4, wave64).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -42,29 +43,27 @@ inline int launch_status(const char *what) {
     return XD_OK;
 }
 
-// Opt-in per-kernel timing (xd_timing_enable): HIP events around the library's own launches,
-// recorded on the launch stream. No cost when disabled.
+// Opt-in per-kernel timing (xd_timing_enable). Every launch goes through launch(): with
+// timing on, the dispatch itself stamps a start/stop event pair (hipExtLaunchKernel), so the
+// recorded time is the kernel's own execution, as a rocprofv3 kernel trace reports it,
+// without the gaps between dispatches. No events and no cost when timing is off.
 bool timing_enabled();
 void timing_record(const char *kernel, hipEvent_t start, hipEvent_t stop);
 
-class KernelTimer {
-  public:
-    KernelTimer(const char *kernel, hipStream_t s) : name_(kernel), s_(s) {
-        if (timing_enabled() && hipEventCreate(&e0_) == hipSuccess && hipEventCreate(&e1_) == hipSuccess)
-            on_ = hipEventRecord(e0_, s_) == hipSuccess;
+// name == nullptr: never timed (the allocation-free entry points create no events).
+template <typename F, typename... Args>
+inline void launch(const char *name, F kernel, dim3 grid, dim3 block, uint32_t shmem, hipStream_t s, Args... args) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (name && timing_enabled()) {
+        if (hipEventCreate(&e0) != hipSuccess) e0 = nullptr;
+        if (e0 && hipEventCreate(&e1) != hipSuccess) {
+            (void)hipEventDestroy(e0);
+            e0 = e1 = nullptr;
+        }
     }
-    ~KernelTimer() {
-        if (on_ && hipEventRecord(e1_, s_) == hipSuccess) timing_record(name_, e0_, e1_);
-    }
-    KernelTimer(const KernelTimer &) = delete;
-    KernelTimer &operator=(const KernelTimer &) = delete;
-
-  private:
-    const char *name_;
-    hipStream_t s_;
-    hipEvent_t e0_ = nullptr, e1_ = nullptr;
-    bool on_ = false;
-};
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, e0, e1, 0u, args...);
+    if (e0) timing_record(name, e0, e1);
+}
 
 // Per-device pass counter used by XD_MODE_ROTATED (advances once per pass).
 unsigned next_rotation(int passes);

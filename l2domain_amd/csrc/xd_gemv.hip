@@ -480,11 +480,12 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
     const int rpw = rows_per_workgroup(M, nv);
     const int nchunks = (M + rpw - 1) / rpw;
     const int grid = ((nchunks + kNumXcd - 1) / kNumXcd) * kNumXcd;
-    const unsigned rot = mode == XD_MODE_ROTATED ? next_rotation(1) : 0u;
+    // rotated: slice s on XCD (s + rot) mod 8 with rot in [1, 8), never the identity placement
+    unsigned rot = mode == XD_MODE_ROTATED ? next_rotation(1) % kNumXcd : 0u;
+    if (mode == XD_MODE_ROTATED && rot == 0) rot = 1;
     hipStream_t s = (hipStream_t)stream;
     const uint4 *A4 = reinterpret_cast<const uint4 *>(A);
     const uint4 *x4 = reinterpret_cast<const uint4 *>(x);
-    KernelTimer kt(F16 ? "gemv_f16f32" : "gemv_f32", s);
     bool done = false;
     // Memory-home routing of 8 KiB row segments when rows are whole multiples of 8 KiB.
     const int S = seg_per_row(K, F16 ? 2 : 4);
@@ -500,10 +501,10 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         sgrid = (sgrid + kNumXcd - 1) / kNumXcd * kNumXcd;
         if (sgrid > (1LL << 30)) return fail(XD_ERR_UNSUPPORTED, "gemv: matrix too large for the split-row route");
         if (S == 2)
-            hipLaunchKernelGGL((gemv_seghome_kernel<F16, true>), dim3((unsigned)sgrid), dim3(kGemvThreads), lds, s, A4, x4,
+            launch("gemv_seghome_kernel", gemv_seghome_kernel<F16, true>, dim3((unsigned)sgrid), dim3(kGemvThreads), lds, s, A4, x4,
                                y, M, S, mode, home, cnt, slot);
         else
-            hipLaunchKernelGGL((gemv_seghome_kernel<F16, false>), dim3((unsigned)sgrid), dim3(kGemvThreads), lds, s, A4,
+            launch("gemv_seghome_kernel", gemv_seghome_kernel<F16, false>, dim3((unsigned)sgrid), dim3(kGemvThreads), lds, s, A4,
                                x4, y, M, S, mode, home, cnt, slot);
         done = true;
     }
@@ -523,10 +524,10 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         long long cgrid = (npairs + 4 * ppw - 1) / (4 * ppw) * 2;
         cgrid = std::max<long long>(kNumXcd, (cgrid + kNumXcd - 1) / kNumXcd * kNumXcd);
         if (cgrid > (1LL << 30)) return fail(XD_ERR_UNSUPPORTED, "gemv: matrix too large for the chunk-home route");
-        hipLaunchKernelGGL((gemv_chunkhome_kernel<F16>), dim3((unsigned)cgrid), dim3(kGemvThreads), lds, s, A4, x4, part,
+        launch("gemv_chunkhome_kernel", gemv_chunkhome_kernel<F16>, dim3((unsigned)cgrid), dim3(kGemvThreads), lds, s, A4, x4, part,
                            M, Hh, mode, home);
         if (int rc = launch_status("gemv_chunkhome_kernel")) return rc;
-        hipLaunchKernelGGL(gemv_pieces_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, s, part, y, M, P);
+        launch("gemv_pieces_kernel", gemv_pieces_kernel, dim3((unsigned)((M + 255) / 256)), dim3(256), 0, s, part, y, M, P);
         done = true;
     }
     // Memory-home routing when every row sits inside one 8 KiB chunk.
@@ -541,7 +542,7 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         done = true;
 #define XD_GEMV_HOME(CC)                                                                                       \
     if (CW == CC) {                                                                                           \
-        hipLaunchKernelGGL((gemv_rowhome_kernel<F16, CC>), dim3(hgrid), dim3(kGemvThreads), lds, s, A4, x4, y, M, \
+        launch("gemv_rowhome_kernel", gemv_rowhome_kernel<F16, CC>, dim3(hgrid), dim3(kGemvThreads), lds, s, A4, x4, y, M, \
                            mode, home);                                                                        \
     } else
         XD_GEMV_HOME(1)
@@ -560,7 +561,7 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         done = true;
 #define XD_GEMV_EXACT(CC, SS, DBB)                                                                        \
     if (CW == CC && S == SS) {                                                                          \
-        hipLaunchKernelGGL((gemv_exact_kernel<F16, CC, SS, DBB>), dim3(grid), dim3(kGemvThreads), lds, s, A4, \
+        launch("gemv_exact_kernel", gemv_exact_kernel<F16, CC, SS, DBB>, dim3(grid), dim3(kGemvThreads), lds, s, A4, \
                            x4, y, M, rpw, nchunks, mode, rot);                                          \
     } else
         XD_GEMV_EXACT(1, 1, true)
@@ -584,10 +585,10 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
     }
     if (!done) {
         if (nv >= kWave * 16) {
-            hipLaunchKernelGGL((gemv_kernel<F16, 16>), dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
+            launch("gemv_kernel", gemv_kernel<F16, 16>, dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
                                nchunks, mode, rot);
         } else {
-            hipLaunchKernelGGL((gemv_kernel<F16, 8>), dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
+            launch("gemv_kernel", gemv_kernel<F16, 8>, dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
                                nchunks, mode, rot);
         }
     }

@@ -44,7 +44,7 @@ extern "C" int xd_gen_zipf_keys(uint32_t *keys, size_t n, const uint64_t *thresh
     if (n == 0) return XD_OK;
     size_t blocks = (n + 255) / 256;
     if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(gen_zipf_keys_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, keys, n,
+    launch("gen_zipf_keys_kernel", gen_zipf_keys_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, keys, n,
                        thresholds, num_bins, seed, scramble);
     return launch_status("gen_zipf_keys_kernel");
 }

@@ -495,8 +495,7 @@ size_t xd_hash_table_bytes(uint64_t slots) { return (size_t)slots * sizeof(Slot)
 
 int xd_hash_init(void *table, uint64_t slots, void *stream) {
     if (int rc = check_table(table, slots)) return rc;
-    KernelTimer kt("hash_init", (hipStream_t)stream);
-    hipLaunchKernelGGL(hash_init_kernel, dim3(grid_for(slots, 8192)), dim3(256), 0, (hipStream_t)stream,
+    launch("hash_init_kernel", hash_init_kernel, dim3(grid_for(slots, 8192)), dim3(256), 0, (hipStream_t)stream,
                        static_cast<Slot *>(table), slots);
     return launch_status("hash_init_kernel");
 }
@@ -508,8 +507,7 @@ int xd_hash_insert_u64(void *table, uint64_t slots, const uint64_t *keys, const 
     XD_REQUIRE(n < (1ull << 32), "xd_hash_insert_u64: n must be < 2^32 per call");
     XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_hash_insert_u64: bad mode");
     if (n == 0) return XD_OK;
-    KernelTimer kt("hash_insert", (hipStream_t)stream);
-    hipLaunchKernelGGL(hash_insert_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+    launch("hash_insert_kernel", hash_insert_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<Slot *>(table), slots - 1, keys, vals, n, mode,
                        HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()}, failed);
     return launch_status("hash_insert_kernel");
@@ -523,8 +521,7 @@ int xd_hash_lookup_u64(const void *table, uint64_t slots, const uint64_t *querie
     XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_hash_lookup_u64: bad mode");
     XD_REQUIRE(n < (1ull << 32), "xd_hash_lookup_u64: n must be < 2^32 per call");
     if (n == 0) return XD_OK;
-    KernelTimer kt("hash_lookup", (hipStream_t)stream);
-    hipLaunchKernelGGL(hash_lookup_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+    launch("hash_lookup_kernel", hash_lookup_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<const Slot *>(table), slots - 1, queries, n, mode,
                        HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()}, vals_out,
                        found_out);
@@ -540,8 +537,7 @@ int xd_dep_probe(const void *table, uint64_t slots, const int32_t *queries, uint
     XD_REQUIRE(chain_len >= 1 && chain_len <= 4096, "xd_dep_probe: chain_len must be in [1, 4096]");
     XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_dep_probe: bad mode");
     if (n == 0) return XD_OK;
-    KernelTimer kt("dep_probe", (hipStream_t)stream);
-    hipLaunchKernelGGL(dep_probe_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+    launch("dep_probe_kernel", dep_probe_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<const int2 *>(table), (uint32_t)(slots - 1), queries, n, chain_len, out, mode,
                        HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()});
     return launch_status("dep_probe_kernel");
@@ -564,16 +560,15 @@ int xd_dep_route(const void *table, uint64_t slots, const int32_t *queries, uint
     uint32_t *bcnt = reinterpret_cast<uint32_t *>(r + L.bcnt);
     const uint64_t base = reinterpret_cast<uint64_t>(table);
     const HomeMap home{home_attr, base / kHomePage, home_mask()};
-    KernelTimer kt("dep_route", s);
     if (n > 0) {
-        hipLaunchKernelGGL(route_count_kernel, dim3((unsigned)L.nblocks), dim3(kHashThreads), 0, s,
+        launch("route_count_kernel", route_count_kernel, dim3((unsigned)L.nblocks), dim3(kHashThreads), 0, s,
                            (uint32_t)(slots - 1), queries, n, home, base, bcnt);
         if (int rc = launch_status("route_count_kernel")) return rc;
     }
-    hipLaunchKernelGGL(route_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, bcnt, L.nblocks, n, header);
+    launch("route_scan_kernel", route_scan_kernel, dim3(1), dim3(kScanThreads), 0, s, bcnt, L.nblocks, n, header);
     if (int rc = launch_status("route_scan_kernel")) return rc;
     if (n == 0) return XD_OK;
-    hipLaunchKernelGGL(route_scatter_kernel, dim3((unsigned)L.nblocks), dim3(kHashThreads), 0, s,
+    launch("route_scatter_kernel", route_scatter_kernel, dim3((unsigned)L.nblocks), dim3(kHashThreads), 0, s,
                        (uint32_t)(slots - 1), queries, n, home, base, bcnt, header,
                        reinterpret_cast<int2 *>(r + L.entries));
     return launch_status("route_scatter_kernel");
@@ -590,8 +585,7 @@ int xd_dep_probe_routed(const void *table, uint64_t slots, const void *route, ui
     if (n == 0) return XD_OK;
     const RouteLayout L = route_layout(n);
     const char *r = static_cast<const char *>(route);
-    KernelTimer kt("dep_probe_routed", (hipStream_t)stream);
-    hipLaunchKernelGGL(dep_probe_routed_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+    launch("dep_probe_routed_kernel", dep_probe_routed_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<const int2 *>(table), (uint32_t)(slots - 1),
                        reinterpret_cast<const int2 *>(r + L.entries), reinterpret_cast<const unsigned long long *>(r),
                        chain_len, out, mode);
@@ -601,7 +595,7 @@ int xd_dep_probe_routed(const void *table, uint64_t slots, const void *route, ui
 int xd_gen_hash_kv(uint64_t *keys, uint64_t *vals, uint64_t n, uint64_t seed, void *stream) {
     XD_REQUIRE(n == 0 || keys != nullptr, "xd_gen_hash_kv: NULL keys");
     if (n == 0) return XD_OK;
-    hipLaunchKernelGGL(gen_hash_kv_kernel, dim3(grid_for(n, 8192)), dim3(256), 0, (hipStream_t)stream, keys, vals, n,
+    launch("gen_hash_kv_kernel", gen_hash_kv_kernel, dim3(grid_for(n, 8192)), dim3(256), 0, (hipStream_t)stream, keys, vals, n,
                        seed);
     return launch_status("gen_hash_kv_kernel");
 }
@@ -610,7 +604,7 @@ int xd_gen_hash_queries(uint64_t *queries, uint64_t n, uint64_t n_keys, uint64_t
     XD_REQUIRE(n == 0 || queries != nullptr, "xd_gen_hash_queries: NULL queries");
     XD_REQUIRE(n_keys > 0, "xd_gen_hash_queries: n_keys must be positive");
     if (n == 0) return XD_OK;
-    hipLaunchKernelGGL(gen_hash_queries_kernel, dim3(grid_for(n, 8192)), dim3(256), 0, (hipStream_t)stream, queries, n,
+    launch("gen_hash_queries_kernel", gen_hash_queries_kernel, dim3(grid_for(n, 8192)), dim3(256), 0, (hipStream_t)stream, queries, n,
                        n_keys, seed, qseed);
     return launch_status("gen_hash_queries_kernel");
 }

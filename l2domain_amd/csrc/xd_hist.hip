@@ -638,74 +638,77 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     const unsigned rot = mode == XD_MODE_ROTATED ? next_rotation(1) % kNumXcd : 0u;
     const unsigned rot_eff = (mode == XD_MODE_ROTATED && rot == 0) ? 1u : rot;  // never the identity
 
-    // Tiles: XCD-aware and rotated calls read the 16 KiB pairs inside the keys as routed
-    // tiles (each group of up to kRouteGroupPairs pairs gives one tile per I/O die); the keys
-    // before the first and after the last pair, and oblivious calls, go in contiguous tiles.
-    int ntl = 0;
+    // Plan every partition launch before enqueuing any, so that a shape the workspace cannot
+    // hold is refused with nothing written. XCD-aware and rotated calls read the 16 KiB pairs
+    // inside the keys as routed tiles (each group of up to kRouteGroupPairs pairs gives one
+    // tile per I/O die); the keys before the first and after the last pair, and oblivious
+    // calls, go in contiguous tiles (one workgroup per tile).
+    const bool pack = L.nb <= kPackBuckets;
+    struct PartLaunch {
+        int kind;     // kPartFull / kPartRange / kPartRouted
+        PartSrc ps;
+        unsigned grid;
+    };
+    PartLaunch plan[5];
+    int nplan = 0, ntl = 0;
+    const HomeMap home{home_attr, reinterpret_cast<uint64_t>(keys) / kHomePage, home_mask()};
+    auto contiguous = [&](size_t r0, size_t r1) {  // tiles of keys [r0, r1)
+        // vector tiles over the whole 16-byte vectors, then the last (r1 - r0) % 4 keys
+        const size_t vend = aligned16(keys + r0) ? r0 + (r1 - r0) / 4 * 4 : r0;
+        if (vend > r0) {
+            const size_t nt = (vend - r0 + kTileKeys - 1) / kTileKeys;
+            plan[nplan++] = PartLaunch{kPartFull, PartSrc{keys, r0, vend, ntl, 0, 0, 0, 0, home}, (unsigned)nt};
+            ntl += (int)nt;
+        }
+        if (vend < r1) {
+            const size_t nt = (r1 - vend + kTileKeys - 1) / kTileKeys;
+            plan[nplan++] = PartLaunch{kPartRange, PartSrc{keys, vend, r1, ntl, 0, 0, 0, 0, home}, (unsigned)nt};
+            ntl += (int)nt;
+        }
+    };
     if (n > 0) {
-        KernelTimer kt("hist_partition", s);
-        const HomeMap home{home_attr, reinterpret_cast<uint64_t>(keys) / kHomePage, home_mask()};
-        const bool pack = L.nb <= kPackBuckets;
-        using PartKernel = void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *);
-        const PartKernel kfull = hist_partition_kernel<kPartFull, false>;
-        const PartKernel kfull_pack = hist_partition_kernel<kPartFull, true>;
-        const PartKernel krouted = hist_partition_kernel<kPartRouted, false>;
-        const PartKernel krouted_pack = hist_partition_kernel<kPartRouted, true>;
-        auto contiguous = [&](size_t r0, size_t r1) -> int {  // tiles of keys [r0, r1)
-            // vector tiles over the whole 16-byte vectors, then the last (r1 - r0) % 4 keys
-            const size_t vend = aligned16(keys + r0) ? r0 + (r1 - r0) / 4 * 4 : r0;
-            if (vend > r0) {
-                const size_t nt = (vend - r0 + kTileKeys - 1) / kTileKeys;
-                PartSrc ps{keys, r0, vend, ntl, 0, 0, 0, 0, home};
-                hipLaunchKernelGGL(pack ? kfull_pack : kfull,
-                                   dim3((unsigned)nt), dim3(kP1Threads), 0, s, ps, num_bins, L.nb, part, offs, tot);
-                if (int rc = launch_status("hist_partition_kernel")) return rc;
-                ntl += (int)nt;
-            }
-            if (vend < r1) {
-                const size_t nt = (r1 - vend + kTileKeys - 1) / kTileKeys;
-                PartSrc ps{keys, vend, r1, ntl, 0, 0, 0, 0, home};
-                hipLaunchKernelGGL((hist_partition_kernel<kPartRange, false>), dim3((unsigned)nt), dim3(kP1Threads), 0, s,
-                                   ps, num_bins, L.nb, part, offs, tot);
-                if (int rc = launch_status("hist_partition_kernel")) return rc;
-                ntl += (int)nt;
-            }
-            return 0;
-        };
         const uint64_t A = reinterpret_cast<uint64_t>(keys);
         const uint64_t pfirst = (A + 16383) / 16384, pend = (A + 4 * (uint64_t)n) / 16384;
         // (the routed kind reads 16-byte vectors counted from key 0: keys must be 16-byte aligned)
         const uint64_t npairs = (mode != XD_MODE_OBLIVIOUS && aligned16(keys) && pend > pfirst) ? pend - pfirst : 0;
         if (npairs == 0) {
-            if (int rc = contiguous(0, n)) return rc;
+            contiguous(0, n);
         } else {
             const uint64_t groups = (npairs + kRouteGroupPairs - 1) / kRouteGroupPairs;
             const size_t head = (size_t)(pfirst * 16384 - A) / 4;
             const size_t tail0 = head + (size_t)npairs * 4096;
             const unsigned grid = (unsigned)((groups + kNumXcd / 2 - 1) / (kNumXcd / 2) * kNumXcd);
-            PartSrc ps{keys, 0, 0, 0, (int)groups, pfirst, npairs, mode, home};
-            hipLaunchKernelGGL(pack ? krouted_pack : krouted,
-                               dim3(grid), dim3(kP1Threads), 0, s, ps, num_bins, L.nb, part, offs, tot);
-            if (int rc = launch_status("hist_partition_kernel")) return rc;
+            plan[nplan++] = PartLaunch{kPartRouted, PartSrc{keys, 0, 0, 0, (int)groups, pfirst, npairs, mode, home}, grid};
             ntl = 2 * (int)groups;
-            if (head > 0)
-                if (int rc = contiguous(0, head)) return rc;
-            if (tail0 < n)
-                if (int rc = contiguous(tail0, n)) return rc;
+            if (head > 0) contiguous(0, head);
+            if (tail0 < n) contiguous(tail0, n);
         }
     }
     if (ntl > L.ntiles) return fail(XD_ERR_WORKSPACE, "xd_hist_u32: tile count exceeds the workspace layout");
-    {
-    KernelTimer kt("hist_count", s);
-    hipLaunchKernelGGL(hist_count_kernel, dim3(L.nitems), dim3(kP2Threads), 0, s, part, offs, L.nb, ntl, tot,
-                       L.per_xcd, partials, buckets, mode, rot_eff);
-    if (int rc = launch_status("hist_count_kernel")) return rc;
+
+    // From the first launch on, an error return leaves the workspace's bucket totals
+    // non-zero: the caller must zero-fill the workspace again before its next use.
+    using PartKernel = void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *);
+    for (int k = 0; k < nplan; ++k) {
+        const PartLaunch &pl = plan[k];
+        PartKernel kern;
+        if (pl.kind == kPartRouted)
+            kern = pack ? hist_partition_kernel<kPartRouted, true> : hist_partition_kernel<kPartRouted, false>;
+        else if (pl.kind == kPartFull)
+            kern = pack ? hist_partition_kernel<kPartFull, true> : hist_partition_kernel<kPartFull, false>;
+        else
+            kern = hist_partition_kernel<kPartRange, false>;
+        launch("hist_partition_kernel", kern, dim3(pl.grid), dim3(kP1Threads), 0, s, pl.ps, num_bins, L.nb, part, offs,
+               tot);
+        if (int rc = launch_status("hist_partition_kernel")) return rc;
     }
-    KernelTimer kt("hist_merge", s);
+    launch("hist_count_kernel", hist_count_kernel, dim3(L.nitems), dim3(kP2Threads), 0, s, part, offs, L.nb, ntl, tot,
+           L.per_xcd, partials, buckets, mode, rot_eff);
+    if (int rc = launch_status("hist_count_kernel")) return rc;
     // one workgroup per merge unit, up to 4096
     const int merge_grid = std::min(std::max(L.nb * kMergeUnitsPerBucket, kNumXcd * 64), 4096);
-    hipLaunchKernelGGL(hist_merge_kernel, dim3(merge_grid), dim3(kMergeThreads), 0, s, partials, buckets, L.nb,
-                       num_bins, counts, aligned16(counts), tot);
+    launch("hist_merge_kernel", hist_merge_kernel, dim3(merge_grid), dim3(kMergeThreads), 0, s, partials, buckets, L.nb,
+           num_bins, counts, aligned16(counts), tot);
     return launch_status("hist_merge_kernel");
 }
 

@@ -254,8 +254,7 @@ int xd_hist256_u32bytes(const uint32_t *words, size_t n, uint32_t *counts, int m
     const uint64_t g8 = (npairs + kNumXcd - 1) / kNumXcd * kNumXcd;
     const int grid = (int)std::min<uint64_t>(kH8MaxGrid, std::max<uint64_t>(kNumXcd, g8));
     const HomeMap home{home_attr, wbeg / kHomePage, home_mask()};
-    KernelTimer kt("hist256", s);
-    hipLaunchKernelGGL(hist256_kernel, dim3(grid), dim3(kH8Threads), 0, s, words, (uint64_t)n, pair0, npairs, mode,
+    launch("hist256_kernel", hist256_kernel, dim3(grid), dim3(kH8Threads), 0, s, words, (uint64_t)n, pair0, npairs, mode,
                        home, reinterpret_cast<unsigned long long *>(ws + L.acc),
                        reinterpret_cast<uint32_t *>(ws + L.sync), counts);
     return launch_status("hist256_kernel");

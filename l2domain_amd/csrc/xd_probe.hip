@@ -144,16 +144,16 @@ int xd_xdom_pchase(int leader_xcd, int follower_xcd, void *chain, size_t chain_b
     hipStream_t s = (hipStream_t)stream;
     uint64_t *c = static_cast<uint64_t *>(chain);
     uint32_t *meta = out + 4 * (size_t)numel;  // [leader xcc, follower xcc, claim, claim]
-    hipLaunchKernelGGL(chase_init_kernel, dim3((numel + 255) / 256), dim3(256), 0, s, c, numel, stride_bytes / 8);
-    hipLaunchKernelGGL(probe_clear_kernel, dim3(1), dim3(64), 0, s, meta, 4);
+    launch("chase_init_kernel", chase_init_kernel, dim3((numel + 255) / 256), dim3(256), 0, s, c, numel, stride_bytes / 8);
+    launch("probe_clear_kernel", probe_clear_kernel, dim3(1), dim3(64), 0, s, meta, 4);
     if (flush_buf) {
         if (int rc = xd_cache_flush(flush_buf, flush_bytes, stream)) return rc;
     }
     // 8 workgroups per XCD so that every XCD surely receives some
     const int grid = 8 * kNumXcd;
-    hipLaunchKernelGGL(pchase_role_kernel, dim3(grid), dim3(64), 0, s, c, numel, leader_xcd, out, meta + 2, meta);
+    launch("pchase_role_kernel", pchase_role_kernel, dim3(grid), dim3(64), 0, s, c, numel, leader_xcd, out, meta + 2, meta);
     if (int rc = launch_status("pchase_role_kernel")) return rc;
-    hipLaunchKernelGGL(pchase_role_kernel, dim3(grid), dim3(64), 0, s, c, numel, follower_xcd, out + 2 * (size_t)numel,
+    launch("pchase_role_kernel", pchase_role_kernel, dim3(grid), dim3(64), 0, s, c, numel, follower_xcd, out + 2 * (size_t)numel,
                        meta + 3, meta + 1);
     return launch_status("pchase_role_kernel");
 }
@@ -166,13 +166,13 @@ int xd_mask_probe(void *buf, size_t bytes, int first_bit, int last_bit, int reps
     hipStream_t s = (hipStream_t)stream;
     const int nb = last_bit - first_bit + 2;  // base address + one entry per bit
     uint32_t *meta = out + 2 * (size_t)nb;    // [die-0 xcc, die-1 xcc, claim, claim]
-    hipLaunchKernelGGL(probe_clear_kernel, dim3(1), dim3(64), 0, s, meta, 4);
+    launch("probe_clear_kernel", probe_clear_kernel, dim3(1), dim3(64), 0, s, meta, 4);
     const int grid = 8 * kNumXcd;
     // XCD 0 sits on I/O die 0, XCD 4 on die 1
-    hipLaunchKernelGGL(mask_probe_kernel, dim3(grid), dim3(64), 0, s, static_cast<uint32_t *>(buf), first_bit, last_bit,
+    launch("mask_probe_kernel", mask_probe_kernel, dim3(grid), dim3(64), 0, s, static_cast<uint32_t *>(buf), first_bit, last_bit,
                        reps, 0, out, meta + 2, meta);
     if (int rc = launch_status("mask_probe_kernel")) return rc;
-    hipLaunchKernelGGL(mask_probe_kernel, dim3(grid), dim3(64), 0, s, static_cast<uint32_t *>(buf), first_bit, last_bit,
+    launch("mask_probe_kernel", mask_probe_kernel, dim3(grid), dim3(64), 0, s, static_cast<uint32_t *>(buf), first_bit, last_bit,
                        reps, kNumXcd / 2, out + nb, meta + 3, meta + 1);
     return launch_status("mask_probe_kernel");
 }

@@ -126,3 +126,12 @@ def mask_probe(first_bit: int = 5, last_bit: int = 29, reps: int = 8, device: in
     return {"bits": bits, "die0_cycles": a[1:], "die1_cycles": b[1:], "base": (int(a[0]), int(b[0])),
             "observed_flip": flip[1:], "active": active, "active_mask": mask,
             "xcc": (int(o[2 * nb]), int(o[2 * nb + 1]))}
+
+
+def read_stream(buf: torch.Tensor, mode: str = "oblivious", home_attr: torch.Tensor | None = None,
+                workgroups: int = 0, depth: int = 0, stream: torch.cuda.Stream | None = None) -> None:
+    """One read of every 16-byte word of `buf` (the roofline probe of cache-resident data):
+    oblivious contiguous, aware near chunks only, rotated far chunks only."""
+    nbytes = buf.numel() * buf.element_size()
+    _lib.call("xd_read_stream", ptr(buf), nbytes, _lib.MODES[mode], ptr(home_attr) if home_attr is not None else None,
+              workgroups, depth, stream_handle(stream))

@@ -89,6 +89,37 @@ def test_workspace_reuse_shrinking_input():
             np.testing.assert_array_equal(gpu_hist(keys, 1 << 20, mode, h), ref)
 
 
+def _hot_case_keys(case: str) -> tuple[np.ndarray, int]:
+    """2^25 keys: more than two tiles per persistent partition workgroup, so every case runs
+    the claim tiles and the read-only-table tiles of the hot-key partition."""
+    n = 1 << 25
+    rng = np.random.default_rng(sum(map(ord, case)))
+    # (the device generator matches the oracle's key by key: test_device_zipf_keys_match_oracle_generator)
+    if case == "zipf_identity":   # hot bins 0, 1, 2, ...: all crowd into bucket 0's slots
+        k = gen.zipf_keys_device(n, 1 << 20, 77, ZIPF_S, scramble=False)
+        return k.cpu().numpy().view(np.uint32).copy(), 1 << 20
+    if case == "zipf_scrambled":  # the config's distribution, with keys past num_bins mixed in
+        k = gen.zipf_keys_device(n, 1 << 20, 78, ZIPF_S).cpu().numpy().view(np.uint32).copy()
+        k[rng.integers(0, n, size=n // 64)] = rng.integers(1 << 20, 1 << 32, size=n // 64, dtype=np.uint64)
+        return k, (1 << 20) - 3
+    if case == "one_bucket":      # every key in bucket 0: at most 256 of them hot
+        return rng.integers(0, 1 << 15, size=n).astype(np.uint32), 1 << 20
+    if case == "few_bins":        # 1000 bins: every key has its own slot
+        return rng.integers(0, 1100, size=n).astype(np.uint32), 1000
+    if case == "one_key":
+        return np.full(n, 123457, dtype=np.uint32), 1 << 20
+    raise ValueError(case)
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("case", ["zipf_identity", "zipf_scrambled", "one_bucket", "few_bins", "one_key"])
+def test_hot_table_cases(case, mode):
+    keys, num_bins = _hot_case_keys(case)
+    ref, _ = ora.histogram(keys, num_bins, nthreads=16)
+    print(case, mode, len(keys), num_bins, flush=True)
+    np.testing.assert_array_equal(gpu_hist(keys, num_bins, mode), ref)
+
+
 @pytest.fixture(scope="module")
 def config_keys():
     keys = gen.zipf_keys_device(HIST_KEYS, HIST_BINS, HIST_SEED, ZIPF_S)

@@ -248,6 +248,17 @@ size_t xd_hist256_workspace_size(void);
 int xd_hist256_u32bytes(const uint32_t *words, size_t n, uint32_t *counts, int mode, const uint8_t *home_attr,
                         void *workspace, size_t workspace_bytes, void *stream);
 
+/* xd_hist256_u32bytes without a caller workspace and without any allocation: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The accumulators and
+ * tickets live in a fixed library array of 8448 bytes per GPU (held until the process ends),
+ * set up and zero-filled on the first call on each device and left zeroed by every call;
+ * the limits are those of xd_hist256_u32bytes (n < 2^30 words), larger inputs are refused
+ * with XD_ERR_INVALID_ARG. Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other host threads) race and must be serialised by the
+ * caller. Never timed by xd_timing_enable (it creates no events). */
+int xd_hist256_u32bytes_noalloc(const uint32_t *words, size_t n, uint32_t *counts, int mode,
+                                const uint8_t *home_attr, void *stream);
 
 /* ------------------------------------------------------------------------------------ */
 /* Hash table: open addressing, linear probing, uint64 keys and values                   */

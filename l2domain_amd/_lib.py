@@ -90,6 +90,7 @@ SIGNATURES: dict[str, tuple] = {
     "xd_hist_u32": (I, [VP, SZ, VP, U32, I, VP, VP, SZ, VP]),
     "xd_hist256_workspace_size": (SZ, []),
     "xd_hist256_u32bytes": (I, [VP, SZ, VP, I, VP, VP, SZ, VP]),
+    "xd_hist256_u32bytes_noalloc": (I, [VP, SZ, VP, I, VP, VP]),
     "xd_hash_table_bytes": (SZ, [U64]),
     "xd_hash_init": (I, [VP, U64, VP]),
     "xd_hash_insert_u64": (I, [VP, U64, VP, VP, U64, I, VP, VP, VP]),

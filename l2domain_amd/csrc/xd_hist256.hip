@@ -36,6 +36,8 @@
 //     accumulators are left zeroed.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "xd_common.hpp"
 
 namespace xd {
@@ -52,11 +54,15 @@ struct H8Layout {
     size_t acc, sync, total;
 };
 
+// 64-bit accumulators of the 8 groups, then 8 group tickets + 1 final ticket
+constexpr size_t kH8AccBytes = (size_t)kNumXcd * kH8Pairs * 8;
+constexpr size_t kH8ScratchBytes = kH8AccBytes + 256;
+
 static H8Layout h8_layout() {
     H8Layout L;
     L.acc = 0;
-    L.sync = L.acc + (size_t)kNumXcd * kH8Pairs * 8;
-    L.total = L.sync + 256;  // 8 group tickets + 1 final ticket
+    L.sync = kH8AccBytes;
+    L.total = kH8ScratchBytes;
     return L;
 }
 
@@ -221,6 +227,45 @@ hist256_kernel(const uint32_t *__restrict__ words, uint64_t n, uint64_t pair0, u
     }
 }
 
+
+// Scratch of the allocation-free entry point (xd_hist256_u32bytes_noalloc): one call's
+// accumulators and tickets, kH8ScratchBytes, one copy per GPU for the life of the process.
+// Host code never uses the array's name as an address: h8_scratch() looks up the device
+// address of this GPU's copy once (hipGetSymbolAddress, with the device current), zero-fills
+// it with a small kernel (not a memset, so a caller may capture the call in a graph) and
+// keeps the address per device. Every call leaves the accumulators and tickets zeroed again.
+static __device__ __align__(256) unsigned char scratch[kH8ScratchBytes];
+
+__global__ void h8_scratch_clear_kernel(uint4 *p, int n16) {
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n16) p[i] = make_uint4(0, 0, 0, 0);
+}
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_h8_mu;
+static void *g_h8_scratch[kMaxDevices];
+
+static int h8_scratch(void **out, hipStream_t s) {
+    int dev = 0;
+    XD_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(XD_ERR_UNSUPPORTED, "xd_hist256_u32bytes_noalloc: device id out of range");
+    std::lock_guard<std::mutex> lk(g_h8_mu);
+    if (g_h8_scratch[dev] == nullptr) {
+        void *p = nullptr;
+        XD_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        static_assert(kH8ScratchBytes % 16 == 0, "scratch in 16-byte words");
+        const int n16 = (int)(kH8ScratchBytes / 16);
+        launch(nullptr, h8_scratch_clear_kernel, dim3((n16 + 255) / 256), dim3(256), 0, s, static_cast<uint4 *>(p), n16);
+        if (int rc = launch_status("h8_scratch_clear_kernel")) return rc;
+        g_h8_scratch[dev] = p;
+    }
+    *out = g_h8_scratch[dev];
+    return XD_OK;
+}
+
+static int hist256_run(const uint32_t *words, size_t n, uint32_t *counts, int mode, const uint8_t *home_attr,
+                       void *workspace, size_t workspace_bytes, void *stream, bool timed);
+
 }  // namespace xd
 
 using namespace xd;
@@ -231,6 +276,22 @@ size_t xd_hist256_workspace_size(void) { return h8_layout().total; }
 
 int xd_hist256_u32bytes(const uint32_t *words, size_t n, uint32_t *counts, int mode, const uint8_t *home_attr,
                         void *workspace, size_t workspace_bytes, void *stream) {
+    return hist256_run(words, n, counts, mode, home_attr, workspace, workspace_bytes, stream, true);
+}
+
+int xd_hist256_u32bytes_noalloc(const uint32_t *words, size_t n, uint32_t *counts, int mode, const uint8_t *home_attr,
+                                void *stream) {
+    void *ws = nullptr;
+    if (int rc = h8_scratch(&ws, (hipStream_t)stream)) return rc;
+    return hist256_run(words, n, counts, mode, home_attr, ws, kH8ScratchBytes, stream, false);
+}
+
+}  // extern "C"
+
+namespace xd {
+
+static int hist256_run(const uint32_t *words, size_t n, uint32_t *counts, int mode, const uint8_t *home_attr,
+                       void *workspace, size_t workspace_bytes, void *stream, bool timed) {
     XD_REQUIRE(counts != nullptr && (reinterpret_cast<uintptr_t>(counts) & 3u) == 0,
                "xd_hist256_u32bytes: counts is NULL or not 4-byte aligned");
     XD_REQUIRE(n == 0 || (words != nullptr && aligned16(words)),
@@ -254,10 +315,11 @@ int xd_hist256_u32bytes(const uint32_t *words, size_t n, uint32_t *counts, int m
     const uint64_t g8 = (npairs + kNumXcd - 1) / kNumXcd * kNumXcd;
     const int grid = (int)std::min<uint64_t>(kH8MaxGrid, std::max<uint64_t>(kNumXcd, g8));
     const HomeMap home{home_attr, wbeg / kHomePage, home_mask()};
-    launch("hist256_kernel", hist256_kernel, dim3(grid), dim3(kH8Threads), 0, s, words, (uint64_t)n, pair0, npairs, mode,
-                       home, reinterpret_cast<unsigned long long *>(ws + L.acc),
-                       reinterpret_cast<uint32_t *>(ws + L.sync), counts);
+    launch(timed ? "hist256_kernel" : nullptr, hist256_kernel, dim3(grid), dim3(kH8Threads), 0, s, words, (uint64_t)n,
+           pair0, npairs, mode, home, reinterpret_cast<unsigned long long *>(ws + L.acc),
+           reinterpret_cast<uint32_t *>(ws + L.sync), counts);
     return launch_status("hist256_kernel");
 }
 
-}  // extern "C"
+}  // namespace xd
+

@@ -99,45 +99,56 @@ __device__ __forceinline__ SlotHome stage_home(const HomeMap &h, uint64_t base, 
     return sh;
 }
 
-// Runs body(item) for every item this wave owns, always on a full wave except for the last
-// batch. In the home modes key_of(i) is read one chunk ahead and keep(key) decides
-// ownership; the kept item indices are compacted into the wave's LDS queue.
+// Runs body(item, key) for every item this wave owns, always on a full wave except for the
+// last batch. key_of(i) is read one chunk ahead; in the home modes keep(key) decides
+// ownership. The kept items' indices and keys are compacted into the wave's LDS queue, so
+// that body() never reads an item's key a second time.
 template <typename KeyOf, typename Keep, typename Body>
-__device__ __forceinline__ void for_each_owned(const Walk &w, uint64_t n, bool filter, uint32_t *queue, KeyOf key_of,
-                                               Keep keep, Body body) {
+__device__ __forceinline__ void for_each_owned(const Walk &w, uint64_t n, bool filter, uint32_t *qidx, uint64_t *qkey,
+                                               KeyOf key_of, Keep keep, Body body) {
     const int lane = lane_id();
     uint32_t fill = 0;  // wave-uniform
     uint64_t c = w.first;
     uint64_t key = 0;
-    if (filter && c * kWave + (uint64_t)lane < n) key = key_of(c * kWave + (uint64_t)lane);
+    if (c * kWave + (uint64_t)lane < n) key = key_of(c * kWave + (uint64_t)lane);
     for (; c * kWave < n; c += w.stride) {
         const uint64_t i = c * kWave + (uint64_t)lane;
         const uint64_t inext = (c + w.stride) * kWave + (uint64_t)lane;
         uint64_t knext = 0;
-        if (filter && inext < n) knext = key_of(inext);
+        if (inext < n) knext = key_of(inext);
         const bool mine = i < n && (!filter || keep(key));
-        key = knext;
         const uint64_t m = __ballot(mine);
-        if (mine) queue[fill + mask_rank(m)] = (uint32_t)i;
+        if (mine) {
+            const uint32_t at = fill + mask_rank(m);
+            qidx[at] = (uint32_t)i;
+            qkey[at] = key;
+        }
+        key = knext;
         fill += (uint32_t)__builtin_popcountll(m);
         __builtin_amdgcn_wave_barrier();
         if (fill >= (uint32_t)kWave) {
-            const uint32_t item = queue[lane];
-            const uint32_t spill = queue[kWave + lane];
-            body((uint64_t)item);
+            const uint32_t item = qidx[lane];
+            const uint64_t ikey = qkey[lane];
+            const uint32_t spill = qidx[kWave + lane];
+            const uint64_t skey = qkey[kWave + lane];
+            body((uint64_t)item, ikey);
             fill -= kWave;
-            if ((uint32_t)lane < fill) queue[lane] = spill;
+            if ((uint32_t)lane < fill) {
+                qidx[lane] = spill;
+                qkey[lane] = skey;
+            }
             __builtin_amdgcn_wave_barrier();
         }
     }
-    if ((uint32_t)lane < fill) body((uint64_t)queue[lane]);
+    if ((uint32_t)lane < fill) body((uint64_t)qidx[lane], qkey[lane]);
 }
 
 __global__ void __launch_bounds__(kHashThreads)
 hash_insert_kernel(Slot *__restrict__ table, uint64_t mask, const uint64_t *__restrict__ keys,
                    const uint64_t *__restrict__ vals, uint64_t n, int mode, HomeMap home,
                    unsigned long long *__restrict__ failed) {
-    __shared__ uint32_t queues[kHashThreads / kWave][2 * kWave];
+    __shared__ uint32_t qidx[kHashThreads / kWave][2 * kWave];
+    __shared__ uint64_t qkey[kHashThreads / kWave][2 * kWave];
     __shared__ uint8_t lattr[kLdsPages];
     const Walk w = make_walk(mode);
     const bool filter = mode != XD_MODE_OBLIVIOUS;
@@ -146,8 +157,7 @@ hash_insert_kernel(Slot *__restrict__ table, uint64_t mask, const uint64_t *__re
     const uint64_t max_probe = mask + 1 < kMaxProbe ? mask + 1 : kMaxProbe;
     auto key_of = [&](uint64_t i) { return keys[i]; };
     auto keep = [&](uint64_t key) { return sh(base + (mix64(key) & mask) * sizeof(Slot)) == w.want; };
-    auto body = [&](uint64_t i) {
-        const uint64_t key = keys[i];
+    auto body = [&](uint64_t i, uint64_t key) {
         if (key == kEmpty) return;
         const uint64_t val = vals[i];
         uint64_t s = mix64(key) & mask;
@@ -167,13 +177,14 @@ hash_insert_kernel(Slot *__restrict__ table, uint64_t mask, const uint64_t *__re
         }
         if (failed) atomicAdd(failed, 1ull);
     };
-    for_each_owned(w, n, filter, queues[threadIdx.x / kWave], key_of, keep, body);
+    for_each_owned(w, n, filter, qidx[threadIdx.x / kWave], qkey[threadIdx.x / kWave], key_of, keep, body);
 }
 
 __global__ void __launch_bounds__(kHashThreads)
 hash_lookup_kernel(const Slot *__restrict__ table, uint64_t mask, const uint64_t *__restrict__ queries, uint64_t n,
                    int mode, HomeMap home, uint64_t *__restrict__ vals_out, uint8_t *__restrict__ found_out) {
-    __shared__ uint32_t queues[kHashThreads / kWave][2 * kWave];
+    __shared__ uint32_t qidx[kHashThreads / kWave][2 * kWave];
+    __shared__ uint64_t qkey[kHashThreads / kWave][2 * kWave];
     __shared__ uint8_t lattr[kLdsPages];
     const Walk w = make_walk(mode);
     const bool filter = mode != XD_MODE_OBLIVIOUS;
@@ -182,8 +193,7 @@ hash_lookup_kernel(const Slot *__restrict__ table, uint64_t mask, const uint64_t
     const uint64_t max_probe = mask + 1 < kMaxProbe ? mask + 1 : kMaxProbe;
     auto key_of = [&](uint64_t i) { return queries[i]; };
     auto keep = [&](uint64_t q) { return sh(base + (mix64(q) & mask) * sizeof(Slot)) == w.want; };
-    auto body = [&](uint64_t i) {
-        const uint64_t q = queries[i];
+    auto body = [&](uint64_t i, uint64_t q) {
         uint64_t s = mix64(q) & mask;
         uint64_t v = 0;
         uint8_t f = 0;
@@ -206,7 +216,7 @@ hash_lookup_kernel(const Slot *__restrict__ table, uint64_t mask, const uint64_t
         vals_out[i] = v;
         found_out[i] = f;
     };
-    for_each_owned(w, n, filter, queues[threadIdx.x / kWave], key_of, keep, body);
+    for_each_owned(w, n, filter, qidx[threadIdx.x / kWave], qkey[threadIdx.x / kWave], key_of, keep, body);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -251,7 +261,8 @@ __device__ __forceinline__ int32_t dep_probe_one(const int2 *__restrict__ table,
 __global__ void __launch_bounds__(kHashThreads)
 dep_probe_kernel(const int2 *__restrict__ table, uint32_t mask, const int32_t *__restrict__ queries, uint64_t n,
                  int chain_len, int32_t *__restrict__ out, int mode, HomeMap home) {
-    __shared__ uint32_t queues[kHashThreads / kWave][2 * kWave];
+    __shared__ uint32_t qidx[kHashThreads / kWave][2 * kWave];
+    __shared__ uint64_t qkey[kHashThreads / kWave][2 * kWave];
     __shared__ uint8_t lattr[kLdsPages];
     const Walk w = make_walk(mode);
     const bool filter = mode != XD_MODE_OBLIVIOUS;
@@ -261,8 +272,8 @@ dep_probe_kernel(const int2 *__restrict__ table, uint32_t mask, const int32_t *_
     auto keep = [&](uint64_t key) {
         return sh(base + (uint64_t)(mix32d((uint32_t)key) & mask) * sizeof(int2)) == w.want;
     };
-    auto body = [&](uint64_t i) {
-        int32_t key = queries[i];
+    auto body = [&](uint64_t i, uint64_t qkey32) {
+        int32_t key = (int32_t)(uint32_t)qkey32;
         uint32_t acc = 0;  // wraps like the reference's int accumulator
         for (int it = 0; it < chain_len; ++it) {
             int32_t nk;
@@ -271,7 +282,7 @@ dep_probe_kernel(const int2 *__restrict__ table, uint32_t mask, const int32_t *_
         }
         out[i] = (int32_t)(acc ^ (uint32_t)key);
     };
-    for_each_owned(w, n, filter, queues[threadIdx.x / kWave], key_of, keep, body);
+    for_each_owned(w, n, filter, qidx[threadIdx.x / kWave], qkey[threadIdx.x / kWave], key_of, keep, body);
 }
 
 // Routed dependent probe: the reference's per-side query lists (HASH.cu:244-270, built on the

@@ -40,6 +40,35 @@ def test_small_table_all_mode_pairs(ins_mode, look_mode):
 
 
 @pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("slots,n", [(8, 5), (1 << 9, 300), (1 << 16, 3 * 4096 + 77), (1 << 20, 9 * 4096 + 1)])
+def test_ragged_batches_repeats_and_empty(slots, n, mode):
+    """Tiny and mid-size tables, batches that are not a multiple of a wave or a workgroup,
+    a key repeated far apart in one batch (one slot, one of its values) and an EMPTY key
+    (skipped)."""
+    keys, vals = ora.hash_kv(n + 40, slots + n)
+    keys = keys[:n].copy()
+    if n > 4096:
+        keys[4100] = keys[3]  # the same key in two tiles
+    keys[n // 2] = EMPTY
+    vals = vals[:n]
+    ref = ora.HashTable(slots)
+    assert ref.build(keys, vals) == 0
+    q = np.concatenate([keys, ora.hash_kv(n + 40, slots + n)[0][n:]])
+    rv, rf = ref.lookup(q)
+    t = HashTable(slots)
+    t.insert(dev(keys), dev(vals), mode=mode)
+    v, f = t.lookup(dev(q), mode=mode)
+    torch.cuda.synchronize()
+    assert t.failures() == 0
+    got_f, got_v = f.cpu().numpy(), host(v)
+    if n > 4096:  # the repeated key keeps one of its two values
+        assert got_f[3] == 1 and got_v[3] in (vals[3], vals[4100])
+        got_v[3] = got_v[4100] = rv[3]
+    np.testing.assert_array_equal(got_f, rf)
+    np.testing.assert_array_equal(got_v, rv)
+
+
+@pytest.mark.parametrize("mode", MODES)
 def test_full_table_failures_and_reinsert(mode):
     slots = 1 << 10
     keys, vals = ora.hash_kv(slots + 50, 5)

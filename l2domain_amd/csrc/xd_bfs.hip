@@ -368,20 +368,24 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
                       next_bits, lvl, my_verts, my_edges);
         }
     } else {
-        // The workgroups of a die walk that die's block list (aware) or the other die's
-        // (rotated), so the neighbour lists are read from the near (far) die.
+        // The XCDs of a die walk that die's block list (aware) or the other die's (rotated),
+        // so the neighbour lists are read from the near (far) die; XCD q of the die owns the
+        // contiguous quarter q of the list in every level, and each of its waves takes two
+        // consecutive list entries, so that the rowptr, level and visited lines of a vertex
+        // range are touched by one XCD only and stay in its L2 from level to level.
         const int b = (int)blockIdx.x;
-        const int per_die = (int)gridDim.x / 2;
-        const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
         const uint32_t die = wg_die(b);
         const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
         const int32_t *mine = blist + (int64_t)want * nblocks;
         const int64_t cnt = (int64_t)bcount[want];
-        const int64_t istride = (int64_t)per_die * kWavesPerWg;
-        for (int64_t i = (int64_t)rank * kWavesPerWg + wave; i < cnt; i += 2 * istride) {
-            const bool hasb = i + istride < cnt;
-            bu_blocks(st, mine[i] * kWave, mine[hasb ? i + istride : i] * kWave, hasb, cur_bits, next_bits, lvl,
-                      my_verts, my_edges);
+        const int q = b % (kNumXcd / 2);  // XCD of the die
+        const int64_t lo = cnt * q / (kNumXcd / 2), hi = cnt * (q + 1) / (kNumXcd / 2);
+        const int64_t wx = (int64_t)(b / kNumXcd) * kWavesPerWg + wave;  // wave of the XCD
+        const int64_t xstride = 2 * (int64_t)(gridDim.x / kNumXcd) * kWavesPerWg;
+        for (int64_t i = lo + 2 * wx; i < hi; i += xstride) {
+            const bool hasb = i + 1 < hi;
+            bu_blocks(st, mine[i] * kWave, mine[hasb ? i + 1 : i] * kWave, hasb, cur_bits, next_bits, lvl, my_verts,
+                      my_edges);
         }
     }
     block_sum2(my_verts, my_edges);
@@ -455,44 +459,51 @@ __global__ void __launch_bounds__(kBfsThreads) bfs_control_kernel(BfsState st, i
 }
 
 // Sorts the 64-vertex blocks by the I/O die that homes the start of their adjacency (the
-// block's first vertex on): list[d * nblocks + i] is the i-th block of die d. The
-// assignment depends only on the graph and the page map, so it is built once per search;
-// the bottom-up steps of the home modes then walk their die's list with no skipped blocks.
-// A workgroup classifies 1024 blocks and reserves its list space with one atomic per die.
+// block's first vertex on): list[d * nblocks + i] is the i-th block of die d, in ascending
+// block order. The assignment depends only on the graph and the page map, so it is built
+// once per graph (one workgroup walks the blocks in order, 1024 at a time); the bottom-up
+// steps of the home modes give each XCD of a die a contiguous quarter of its die's list.
 constexpr int kBlkThreads = 1024;
 __global__ void __launch_bounds__(kBlkThreads)
 bfs_blocks_kernel(const int32_t *__restrict__ rowptr, int64_t nblocks, uint64_t cbase, int64_t col_bytes,
                   HomeMap home, int32_t *__restrict__ list, unsigned long long *__restrict__ count) {
     __shared__ uint32_t wcnt[2][kBlkThreads / kWave];
-    __shared__ unsigned long long wbase[2][kBlkThreads / kWave];
+    __shared__ uint32_t wbase[2][kBlkThreads / kWave];
+    __shared__ unsigned long long base[2];
     const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-    const int64_t blk = (int64_t)blockIdx.x * kBlkThreads + tid;
-    uint32_t d = 2;
-    if (blk < nblocks) {
-        uint64_t off = (uint64_t)rowptr[blk * kWave] * sizeof(int32_t);
-        if (off >= (uint64_t)col_bytes) off = (uint64_t)col_bytes - 1;  // trailing isolated vertices
-        d = home(cbase + off);
-    }
-    const uint64_t m0 = __ballot(d == 0), m1 = __ballot(d == 1);
-    if (lane == 0) {
-        wcnt[0][wave] = (uint32_t)__builtin_popcountll(m0);
-        wcnt[1][wave] = (uint32_t)__builtin_popcountll(m1);
-    }
+    if (tid < 2) base[tid] = 0ull;
     __syncthreads();
-    if (tid < 2) {
-        unsigned long long tot = 0;
-        for (int w = 0; w < kBlkThreads / kWave; ++w) {
-            wbase[tid][w] = tot;
-            tot += wcnt[tid][w];
+    for (int64_t blk0 = 0; blk0 < nblocks; blk0 += kBlkThreads) {
+        const int64_t blk = blk0 + tid;
+        uint32_t d = 2;
+        if (blk < nblocks) {
+            uint64_t off = (uint64_t)rowptr[blk * kWave] * sizeof(int32_t);
+            if (off >= (uint64_t)col_bytes) off = (uint64_t)col_bytes - 1;  // trailing isolated vertices
+            d = home(cbase + off);
         }
-        const unsigned long long b = tot ? atomicAdd(&count[tid], tot) : 0ull;
-        for (int w = 0; w < kBlkThreads / kWave; ++w) wbase[tid][w] += b;
+        const uint64_t m0 = __ballot(d == 0), m1 = __ballot(d == 1);
+        if (lane == 0) {
+            wcnt[0][wave] = (uint32_t)__builtin_popcountll(m0);
+            wcnt[1][wave] = (uint32_t)__builtin_popcountll(m1);
+        }
+        __syncthreads();
+        if (tid < 2) {
+            uint32_t tot = 0;
+            for (int w = 0; w < kBlkThreads / kWave; ++w) {
+                wbase[tid][w] = tot;
+                tot += wcnt[tid][w];
+            }
+        }
+        __syncthreads();
+        if (d < 2) {
+            const uint64_t m = d ? m1 : m0;
+            list[(int64_t)d * nblocks + (int64_t)(base[d] + wbase[d][wave] + mask_rank(m))] = (int32_t)blk;
+        }
+        __syncthreads();
+        if (tid < 2) base[tid] += wbase[tid][kBlkThreads / kWave - 1] + wcnt[tid][kBlkThreads / kWave - 1];
+        __syncthreads();
     }
-    __syncthreads();
-    if (d < 2) {
-        const uint64_t m = d ? m1 : m0;
-        list[(int64_t)d * nblocks + (int64_t)(wbase[d][wave] + mask_rank(m))] = (int32_t)blk;
-    }
+    if (tid < 2) count[tid] = base[tid];
 }
 
 __global__ void bfs_clear2_kernel(unsigned long long *p) {
@@ -508,7 +519,7 @@ static int build_route(const int32_t *rowptr, const int32_t *col, int32_t V, int
     launch("bfs_clear2_kernel", bfs_clear2_kernel, dim3(1), dim3(64), 0, s, bcount);
     if (nnz == 0) return launch_status("bfs_clear2_kernel");
     const HomeMap home{home_attr, reinterpret_cast<uint64_t>(col) / kHomePage, home_mask()};
-    launch("bfs_blocks_kernel", bfs_blocks_kernel, dim3((unsigned)((nblocks + kBlkThreads - 1) / kBlkThreads)), dim3(kBlkThreads),
+    launch("bfs_blocks_kernel", bfs_blocks_kernel, dim3(1), dim3(kBlkThreads),
                        0, s, rowptr, nblocks, reinterpret_cast<uint64_t>(col), nnz * (int64_t)sizeof(int32_t), home, blist,
                        bcount);
     return launch_status("bfs_blocks_kernel");

@@ -145,6 +145,45 @@ int xd_xdom_pchase(int leader_xcd, int follower_xcd, void *chain, size_t chain_b
  * below 21 are page-stable (2 MiB pages). */
 int xd_mask_probe(void *buf, size_t bytes, int first_bit, int last_bit, int reps, uint32_t *out, void *stream);
 
+/* DomainScan latency curves (run_figure_3, architecture/src/architecture_probe.cu:598-631,
+ * on measure_offsets :417-458): after a cache flush (flush_buf of xd_cache_flush_bytes(), or
+ * NULL for none), the first workgroup on XCD `leader_xcd` loads buf + 2^b for b in
+ * [first_bit, last_bit]; then the first workgroup running on the compute unit `follower_cu`
+ * times one load of each address, in that order. follower_cu is a placement key
+ * (xcc << 16) | (se << 8) | (sh << 4) | cu: an xd_domain_scan word shifted right by 8. The
+ * leader hands over at the kernel boundary (L2 and Infinity Cache contents survive it). out
+ * (device, uint32): [last_bit - first_bit + 1] follower cycles, then [leader found, follower
+ * found, leader XCC, 0]: a 0 in either flag means no workgroup ran there and the curve is
+ * unwritten. buf: device, 8-byte aligned, at least 2^last_bit + 8 bytes. */
+int xd_domain_scan_latency(void *buf, size_t bytes, int first_bit, int last_bit, int leader_xcd, uint32_t follower_cu,
+                           const void *flush_buf, size_t flush_bytes, uint32_t *out, void *stream);
+
+/* Channel probe, the MaskProbe search for the address bits that select an L2 channel of an
+ * XCD (measure_offsets / run_mask_probe, architecture/src/architecture_probe.cu:417-458,
+ * 644-686; k_get_mask, utility/get_mask.cu:87-150, which find the bits that pick an H100 L2
+ * partition). A query times a set of 64 lines: lane i of 128 one-wave workgroups on XCD
+ * `xcd` reads base + (XOR of vecs[k] over the set bits k of i), `iters` times, with loads
+ * that skip the vector L1 and hit the L2. A channel serves its lines one after another, so
+ * the time grows with the largest number of lines sharing a channel. base = buf rounded up to
+ * 2 MiB (buf device; bytes must still cover the span after the rounding). Times are HIP-event
+ * minima of three launches on `stream`; the calls wait for them.
+ *
+ * xd_channel_time: one query. vecs (host, 6 entries): multiples of 128 below 2^40.
+ *
+ * xd_channel_probe: recovers the channel-select functions as XOR masks of address bits in
+ * [bit0, bit1] (7 <= bit0, bit0 + 6 <= bit1 < 34). out_window_us[bit1 - bit0 - 4]: the windows
+ * of six consecutive bits b..b+5, b = bit0.. ; out_fast_us: the fastest time seen (every
+ * channel in use). Then up to max_sets five-bit sets F in a fixed pseudo-random order: a set
+ * whose image has rank one below the maximum gives, per added bit f, T_fast when f is in the
+ * mask of the one channel function that is constant on F, 2 T_fast otherwise. Each new mask
+ * (GF(2)-independent of those found) goes to out_masks[k] (up to 4) with its curve
+ * out_curves[k * (bit1 - bit0 + 1) + (f - bit0)] (microseconds; 0 for the bits of F);
+ * *out_nmasks = how many. */
+int xd_channel_time(void *buf, size_t bytes, int xcd, const uint64_t *vecs, int iters, float *out_us, void *stream);
+int xd_channel_probe(void *buf, size_t bytes, int xcd, int bit0, int bit1, int iters, int max_sets,
+                     float *out_window_us, float *out_fast_us, uint64_t *out_masks, float *out_curves, int *out_nmasks,
+                     void *stream);
+
 /* Bytes of read traffic xd_cache_flush needs to evict 8 x 4 MB L2 and the 256 MB
  * Infinity Cache (>= 4x their sum). */
 size_t xd_cache_flush_bytes(void);

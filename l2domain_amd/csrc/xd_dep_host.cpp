@@ -66,7 +66,7 @@ int xd_dep_make_keys(uint64_t table_addr, uint64_t slots, const uint8_t *home_at
     for (; n < K; ++n) {
         if (cand > INT32_MAX) return XD_ERR_UNSUPPORTED;
         keys[n] = (int32_t)cand;
-        nexts[n] = (int32_t)cand;  // cold keys loop on themselves
+        nexts[n] = (int32_t)cand;  // a cold key is its own successor: its chain stays put
         cand += 2;
     }
     return XD_OK;

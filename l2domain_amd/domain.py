@@ -88,6 +88,40 @@ def xdom_pchase(leader_xcd: int, follower_xcd: int, numel: int = 2048, stride: i
             "follower_first": o[2 * numel:3 * numel].copy(), "follower_second": o[3 * numel:4 * numel].copy()}
 
 
+def compute_units(device: int = 0, num_wg: int = 4096) -> list[int]:
+    """Placement keys (xcc << 16) | (se << 8) | (sh << 4) | cu of every compute unit that a
+    DomainScan of `num_wg` workgroups reaches, sorted (XCD-major)."""
+    words = domain_scan(num_wg, device).numpy().view("uint32")
+    return sorted({int(w) >> 8 for w in words})
+
+
+def domain_scan_latency(first_bit: int = 7, last_bit: int = 31, leader_xcd: int = 0, followers=None,
+                        flush: bool = True, device: int = 0) -> dict:
+    """DomainScan latency curves (run_figure_3, architecture_probe.cu:598-631): for every
+    follower compute unit (placement keys; default all that compute_units() finds), the cycles
+    of one load of buf + 2^b, b = first_bit..last_bit, right after a leader workgroup on XCD
+    `leader_xcd` loaded the same addresses. As in the reference (measure_offsets :440-448) the
+    whole protocol -- cache flush, leader, follower -- runs twice per follower and the second
+    curve is kept. Returns {"bits": [...], "curves": {key: np.ndarray}}."""
+    dev = f"cuda:{device}"
+    keys = compute_units(device) if followers is None else [int(k) for k in followers]
+    nbytes = (1 << last_bit) + 4096
+    buf = torch.zeros(nbytes // 4, dtype=torch.int32, device=dev)
+    nb = last_bit - first_bit + 1
+    out = torch.zeros(nb + 4, dtype=torch.int32, device=dev)
+    fl = CacheFlusher(device) if flush else None
+    curves = {}
+    for key in keys:
+        for _ in range(2):
+            _lib.call("xd_domain_scan_latency", ptr(buf), nbytes, first_bit, last_bit, leader_xcd, key,
+                      ptr(fl.buf) if fl else None, fl.bytes if fl else 0, ptr(out), stream_handle())
+        o = out.cpu().numpy().view("uint32")
+        if o[nb] != 1 or o[nb + 1] != 1:
+            raise RuntimeError(f"domain_scan_latency: no workgroup ran on the leader XCD or on CU key {key:#x}")
+        curves[key] = o[:nb].copy()
+    return {"bits": list(range(first_bit, last_bit + 1)), "leader_xcd": leader_xcd, "curves": curves}
+
+
 def derive_active_bits(a_curve, b_curve) -> list[bool]:
     """The reference's rule (derive_active_bits, architecture_probe.cu:495-523): the relation
     a > b / a < b of the base entry (or the first unequal one) is the baseline; an entry is
@@ -135,3 +169,67 @@ def read_stream(buf: torch.Tensor, mode: str = "oblivious", home_attr: torch.Ten
     nbytes = buf.numel() * buf.element_size()
     _lib.call("xd_read_stream", ptr(buf), nbytes, _lib.MODES[mode], ptr(home_attr) if home_attr is not None else None,
               workgroups, depth, stream_handle(stream))
+
+
+def _channel_buffer(top_bit: int, device: int):
+    """A buffer whose start the library rounds up to 2 MiB, holding offsets below 2^(top_bit+1)."""
+    nbytes = (2 << top_bit) + (2 << 20)
+    return torch.zeros(nbytes // 4, dtype=torch.int32, device=f"cuda:{device}"), nbytes
+
+
+def channel_time(vecs, xcd: int = 0, iters: int = 256, device: int = 0) -> float:
+    """One channel-probe query (xd_channel_time): microseconds for 128 waves on XCD `xcd` to
+    read, `iters` times, the 64 lines base + XOR of the six address vectors `vecs` picked by
+    the lane bits."""
+    vecs = [int(x) for x in vecs]
+    assert len(vecs) == 6
+    buf, nbytes = _channel_buffer(max(max(vecs).bit_length() - 1, 7), device)
+    vv = (C.c_uint64 * 6)(*vecs)
+    us = C.c_float(0.0)
+    torch.cuda.synchronize()
+    _lib.call("xd_channel_time", ptr(buf), nbytes, xcd, vv, iters, C.byref(us), stream_handle())
+    return float(us.value)
+
+
+def gf2_rank(vectors) -> int:
+    """Rank over GF(2) of integers read as bit vectors."""
+    basis = []
+    for v in vectors:
+        for b in basis:
+            v = min(v, v ^ b)
+        if v:
+            basis.append(v)
+    return len(basis)
+
+
+def channel_of(addr: int, masks) -> int:
+    """Channel index of an address under XOR masks: bit k = parity of addr & masks[k]."""
+    return sum((bin(addr & m).count("1") & 1) << k for k, m in enumerate(masks))
+
+
+def channel_probe(xcd: int = 0, bits=(7, 20), iters: int = 256, max_sets: int = 256, device: int = 0) -> dict:
+    """Channel probe (xd_channel_probe): the XOR masks of address bits that select the L2 channel
+    of a line on one XCD. `window_us[b - bits[0]]` times the 64 lines spanned by bits b..b+5;
+    `masks` are GF(2)-independent channel-select functions, each with the per-bit curve it was
+    read from; `active_mask` is every bit that enters some function (a bit outside it never
+    changes the channel). Only bits <= 20 (inside a 2 MiB page) mean the same in virtual and
+    physical addresses."""
+    b0, b1 = bits
+    buf, nbytes = _channel_buffer(b1, device)
+    nb, nw = b1 - b0 + 1, b1 - b0 - 4
+    win = (C.c_float * nw)()
+    fast = C.c_float(0.0)
+    masks = (C.c_uint64 * 4)()
+    curves = (C.c_float * (4 * nb))()
+    nm = C.c_int(0)
+    torch.cuda.synchronize()
+    _lib.call("xd_channel_probe", ptr(buf), nbytes, xcd, b0, b1, iters, max_sets, win, C.byref(fast), masks, curves,
+              C.byref(nm), stream_handle())
+    k = int(nm.value)
+    ms = [int(masks[i]) for i in range(k)]
+    active = 0
+    for m in ms:
+        active |= m
+    return {"xcd": xcd, "bits": list(range(b0, b1 + 1)), "window_bits": list(range(b0, b0 + nw)),
+            "window_us": list(win), "fast_us": float(fast.value), "masks": ms,
+            "curves": [list(curves[i * nb:(i + 1) * nb]) for i in range(k)], "active_mask": active}

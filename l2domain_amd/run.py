@@ -3,7 +3,7 @@
     python -m l2domain_amd.run APP [--preset quick|paper] [--device auto|INDEX|UUID]
                                [--build-only] [--dry-run] [--arch auto|gfx950]
                                [--wait-timeout SEC] [--poll-interval SEC] [--output-dir PATH]
-                               [--figure 2|4] [--peer A,B]
+                               [--figure 2|3|4] [--peer A,B]
 
 APP is gemv, histogram, hash, bfs (applications/*/run.sh) or architecture (the probe
 figures of architecture/run_figure_0N.sh). Options, presets, case lists, CSV file names,
@@ -440,22 +440,31 @@ def run_bfs(args, run, out_dir: Path):
 
 def run_architecture(args, run, out_dir: Path):
     """architecture/_run_figure.sh for the figures this build measures: 2 (XDom-PChase, the
-    leader/follower chase) and 4 (MaskProbe); DomainScan's workgroup -> XCD map goes beside."""
+    leader/follower chase), 3 (DomainScan latency curves of every compute unit after a leader
+    on XCD 0) and 4 (MaskProbe, with the L2 channel functions beside it in
+    figure_04_channels.csv); DomainScan's workgroup -> XCD map goes beside every figure."""
     tag = "%02d" % args.figure
     data = out_dir / "data"
     csv = data / f"figure_{tag}.csv"
     if not args.dry_run:
         data.mkdir(parents=True, exist_ok=True)
         csv.unlink(missing_ok=True)
+    st1 = 0
     if args.figure == 2:
         leader, follower = (0, 4) if args.peer == "auto" else map(int, args.peer.split(","))
         st, _ = run("xd_arch_probe", "pchase", leader, follower, 2048, 128, f"--csv={csv}")
+    elif args.figure == 3:
+        st, _ = run("xd_arch_probe", "scanlat", 7, 31, 0, f"--csv={csv}")
     else:
         st, _ = run("xd_arch_probe", "maskprobe", 5, 29, 8, f"--csv={csv}")
+        chan = data / "figure_04_channels.csv"
+        if not args.dry_run:
+            chan.unlink(missing_ok=True)
+        st1, _ = run("xd_arch_probe", "chanprobe", 0, 7, 20, f"--csv={chan}")
     st2, _ = run("xd_arch_probe", "domainscan", 4096, f"--csv={data / 'domainscan.csv'}")
     if not args.dry_run:
         print(f"Figure {tag} CSV: {csv}")
-    return (1 if st else 0) + (1 if st2 else 0)
+    return (1 if st else 0) + (1 if st1 else 0) + (1 if st2 else 0)
 
 
 APP_FUNCS = {"gemv": run_gemv, "histogram": run_histogram, "hash": run_hash, "bfs": run_bfs,
@@ -474,7 +483,7 @@ def parse(argv):
     ap.add_argument("--wait-timeout", type=int, default=1800, help="wait for a free GPU (seconds, default 1800)")
     ap.add_argument("--poll-interval", type=int, default=10, help="GPU polling interval (seconds, default 10)")
     ap.add_argument("--output-dir", default=None, help="runtime output directory (default: out/APP)")
-    ap.add_argument("--figure", type=int, default=2, help="architecture: figure 2 or 4")
+    ap.add_argument("--figure", type=int, default=2, help="architecture: figure 2, 3 or 4")
     ap.add_argument("--peer", default="auto", help="architecture figure 2: leader,follower XCD pair")
     args = ap.parse_args(argv)
     if args.preset not in ("quick", "paper"):
@@ -485,8 +494,8 @@ def parse(argv):
         raise UsageError("--arch must be auto or gfx950 (this build targets MI355X only)")
     if args.device != "auto" and not re.fullmatch(r"\d+|[0-9A-Za-z_-]{8,}", args.device):
         raise UsageError("--device must be auto, a physical index or a unique id")
-    if args.figure not in (2, 4):
-        raise UsageError("--figure must be 2 or 4")
+    if args.figure not in (2, 3, 4):
+        raise UsageError("--figure must be 2, 3 or 4")
     if args.peer != "auto" and (args.figure != 2 or not re.fullmatch(r"[0-7],[0-7]", args.peer)):
         raise UsageError("--peer must be A,B with XCD ids in [0, 8), and only for figure 2")
     if args.output_dir == "":

@@ -1,10 +1,20 @@
-// Architecture probe runner: DomainScan, XDom-PChase and MaskProbe with the CSV schemas of
-// the reference's architecture figures (architecture/src/architecture_probe.cu: figure 2
-// columns :587, figure 4 columns of run_figure_4; data in architecture/data/figure_0*.csv).
+// Architecture probe runner: DomainScan, XDom-PChase, MaskProbe and the L2 channel probe with
+// the CSV schemas of the reference's architecture figures (architecture/src/
+// architecture_probe.cu: figure 2 columns :587, figure 3 columns :613, figure 4 columns of
+// run_figure_4; data in architecture/data/figure_0*.csv).
 //
 //   xd_arch_probe domainscan [num_wg=4096]                          [--csv=FILE]
+//   xd_arch_probe scanlat [first_bit=7] [last_bit=31] [leader_xcd=0] [--csv=FILE]
 //   xd_arch_probe pchase [leader_xcd=0] [follower_xcd=4] [numel=2048] [stride=128] [--csv=FILE]
 //   xd_arch_probe maskprobe [first_bit=5] [last_bit=29] [reps=8]    [--csv=FILE]
+//   xd_arch_probe chanprobe [xcd=0] [first_bit=7] [last_bit=20]     [--csv=FILE]
+//
+// scanlat (figure 3): for every compute unit in turn, a flushed-cache leader/follower round
+// (xd_domain_scan_latency) run twice, the second kept; tpc_id = follower index, resource_id =
+// its placement key, tpc_sm0 = its XCD, tpc_sm1 = its rank inside the XCD, follower_sm = its
+// global index XCD * 32 + rank. chanprobe: the L2 channel functions of one XCD as XOR masks;
+// rows per (function, bit) with the time of the bit added to the function's five-bit set
+// (function -1: the windows of six consecutive bits starting at address_bit).
 //
 // The SM columns of the reference's schemas (leader_sm, follower_sm, sm_a, sm_b) carry XCD
 // ids here: the XCD is the L2 domain on MI355X. pchase flushes every L2 and the Infinity
@@ -25,9 +35,11 @@ static double med(const uint32_t *p, int n) {
 int main(int argc, char **argv) {
     Options o(argc, argv);
     const std::string what = o.gets(0, "");
-    if (o.help || (what != "domainscan" && what != "pchase" && what != "maskprobe")) {
-        printf("usage: %s domainscan [num_wg] | pchase [leader_xcd] [follower_xcd] [numel] [stride] | "
-               "maskprobe [first_bit] [last_bit] [reps]  [--csv=FILE]\n",
+    if (o.help || (what != "domainscan" && what != "scanlat" && what != "pchase" && what != "maskprobe" &&
+                   what != "chanprobe")) {
+        printf("usage: %s domainscan [num_wg] | scanlat [first_bit] [last_bit] [leader_xcd] | pchase [leader_xcd] "
+               "[follower_xcd] [numel] [stride] | maskprobe [first_bit] [last_bit] [reps] | chanprobe [xcd] "
+               "[first_bit] [last_bit]  [--csv=FILE]\n",
                argv[0]);
         return o.help ? 0 : 2;
     }
@@ -59,6 +71,103 @@ int main(int argc, char **argv) {
                per[1], per[2], per[3], per[4], per[5], per[6], per[7]);
         (void)hipFree(d);
         return rr == nwg ? 0 : 3;
+    }
+    if (what == "scanlat") {
+        const int b0 = (int)o.geti(1, 7), b1 = (int)o.geti(2, 31), leader = (int)o.geti(3, 0);
+        if (b0 < 3 || b1 < b0 || b1 > 34 || leader < 0 || leader > 7) return 2;
+        // the compute units a DomainScan reaches, XCD-major
+        const int nwg = 4096;
+        uint32_t *d;
+        RUN_HIP(hipMalloc(&d, (size_t)nwg * 4));
+        RUN_XD(xd_domain_scan(nwg, d, s));
+        std::vector<uint32_t> w(nwg);
+        RUN_HIP(hipMemcpy(w.data(), d, (size_t)nwg * 4, hipMemcpyDeviceToHost));
+        (void)hipFree(d);
+        std::vector<uint32_t> keys;
+        for (uint32_t x : w) keys.push_back(x >> 8);
+        std::sort(keys.begin(), keys.end());
+        keys.erase(std::unique(keys.begin(), keys.end()), keys.end());
+        const int nb = b1 - b0 + 1;
+        const size_t bytes = (1ull << b1) + 4096;
+        void *buf;
+        uint32_t *out;
+        RUN_HIP(hipMalloc(&buf, bytes));
+        RUN_HIP(hipMemset(buf, 0, bytes));
+        RUN_HIP(hipMalloc(&out, (size_t)(nb + 4) * 4));
+        Flusher fl;
+        std::vector<uint32_t> h(nb + 4);
+        std::vector<double> same, other;
+        int rank = 0;
+        uint32_t prev_xcd = 0xffffffffu;
+        for (size_t t = 0; t < keys.size(); ++t) {
+            const uint32_t xcd = keys[t] >> 16;
+            rank = xcd == prev_xcd ? rank + 1 : 0;
+            prev_xcd = xcd;
+            for (int rep = 0; rep < 2; ++rep)
+                RUN_XD(xd_domain_scan_latency(buf, bytes, b0, b1, leader, keys[t], fl.buf, fl.bytes, out, s));
+            RUN_HIP(hipMemcpy(h.data(), out, h.size() * 4, hipMemcpyDeviceToHost));
+            if (h[nb] != 1 || h[nb + 1] != 1) {
+                fprintf(stderr, "scanlat: no workgroup on the leader XCD or on CU key 0x%x\n", keys[t]);
+                return 3;
+            }
+            std::vector<float> c(h.begin(), h.begin() + nb);
+            ((int)xcd == leader ? same : other).push_back(median(c));
+            for (int k = 0; k < nb; ++k)
+                csv_append(o.csv,
+                           "device_index,device_name,leader_sm,tpc_id,resource_id,tpc_sm0,tpc_sm1,follower_sm,"
+                           "address_bit,latency_cycles",
+                           dev + "," + std::to_string(h[nb + 2]) + "," + std::to_string(t) + "," +
+                               std::to_string(keys[t]) + "," + std::to_string(xcd) + "," + std::to_string(rank) +
+                               "," + std::to_string(xcd * 32 + rank) + "," + std::to_string(b0 + k) + "," +
+                               std::to_string(h[k]));
+        }
+        auto avg = [](const std::vector<double> &v) {
+            double a = 0;
+            for (double x : v) a += x;
+            return v.empty() ? 0.0 : a / v.size();
+        };
+        printf("scanlat followers=%zu bits=%d..%d leader_xcd=%d mean_median_cycles same_xcd=%.0f other_xcd=%.0f\n",
+               keys.size(), b0, b1, leader, avg(same), avg(other));
+        (void)hipFree(buf);
+        (void)hipFree(out);
+        return 0;
+    }
+    if (what == "chanprobe") {
+        const int xcd = (int)o.geti(1, 0), b0 = (int)o.geti(2, 7), b1 = (int)o.geti(3, 20);
+        if (xcd < 0 || xcd > 7 || b0 < 7 || b1 - b0 < 6 || b1 > 33) return 2;
+        const size_t bytes = (2ull << b1) + (2ull << 20);
+        void *buf;
+        RUN_HIP(hipMalloc(&buf, bytes));
+        RUN_HIP(hipMemset(buf, 0, bytes));
+        const int nb = b1 - b0 + 1, nw = b1 - b0 - 4;
+        std::vector<float> win(nw), curves(4 * (size_t)nb);
+        float fast = 0.0f;
+        uint64_t masks[4] = {0, 0, 0, 0};
+        int nm = 0;
+        RUN_XD(xd_channel_probe(buf, bytes, xcd, b0, b1, 256, 256, win.data(), &fast, masks, curves.data(), &nm, s));
+        const char *hdr = "device_index,device_name,xcd,function,mask,address_bit,us,in_function,page_stable";
+        for (int k = 0; k < nw; ++k)
+            csv_append(o.csv, hdr,
+                       dev + "," + std::to_string(xcd) + ",-1,0," + std::to_string(b0 + k) + "," +
+                           std::to_string(win[k]) + ",0," + std::to_string((int)(b0 + k + 5 <= 20)));
+        uint64_t active = 0;
+        std::string ms;
+        for (int f = 0; f < nm; ++f) {
+            active |= masks[f];
+            char hx[32];
+            snprintf(hx, sizeof hx, "0x%llx", (unsigned long long)masks[f]);
+            ms += (ms.empty() ? "" : ",") + std::string(hx);
+            for (int k = 0; k < nb; ++k)
+                csv_append(o.csv, hdr,
+                           dev + "," + std::to_string(xcd) + "," + std::to_string(f) + "," + hx + "," +
+                               std::to_string(b0 + k) + "," + std::to_string(curves[(size_t)f * nb + k]) + "," +
+                               std::to_string((int)(masks[f] >> (b0 + k) & 1)) + "," +
+                               std::to_string((int)(b0 + k <= 20)));
+        }
+        printf("chanprobe xcd=%d bits=%d..%d fast_us=%.1f functions=%d masks=%s active_mask=0x%llx\n", xcd, b0, b1,
+               fast, nm, ms.c_str(), (unsigned long long)active);
+        (void)hipFree(buf);
+        return nm > 0 ? 0 : 3;
     }
     if (what == "pchase") {
         const int a = (int)o.geti(1, 0), b = (int)o.geti(2, 4), n = (int)o.geti(3, 2048), stride = (int)o.geti(4, 128);

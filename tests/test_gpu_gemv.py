@@ -135,6 +135,22 @@ def test_f16_integer_inputs_exact():
         np.testing.assert_array_equal(run(W, x, mode), ref)
 
 
+@pytest.mark.parametrize("dtype,M,K", [(np.float16, 34, 14336), (np.float16, 4096, 14336), (np.float32, 34, 3072),
+                                       (np.float32, 4096, 7168), (np.float32, 64, 4096), (np.float32, 64, 8192),
+                                       (np.float16, 64, 8192)])
+@pytest.mark.parametrize("mode", MODES)
+def test_home_routes_integer_exact(dtype, M, K, mode):
+    """The memory-home routes through the workspace: rows of an odd number of 4 KiB halves
+    (chunk route: 28 KiB fp16 and fp32 rows, 12 KiB fp32 rows) and rows of whole 8 KiB chunks
+    (split-row route). A dropped, doubled or misplaced 16-byte vector changes an integer sum,
+    which is exact in fp32 here (|w| <= 8, |x| <= 3, K <= 14336: |y| < 2^24)."""
+    rng = np.random.default_rng(M * 131 + K)
+    W = rng.integers(-8, 9, size=(M, K)).astype(dtype)
+    x = rng.integers(-3, 4, size=K).astype(dtype)
+    ref = (W.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)
+    np.testing.assert_array_equal(run(W, x, mode, mapped=True), ref)
+
+
 def test_f16_row_home_modes_bit_identical():
     # up-projection rows are 8 KiB: the aware/rotated modes route whole rows by home die and
     # must reproduce the oblivious kernel bit for bit (same per-row summation order)

@@ -20,7 +20,7 @@ def call(*args):
 
 
 @pytest.mark.parametrize("bad", [["gemv", "--preset", "huge"], ["bfs", "--arch", "sm_90a"],
-                                 ["architecture", "--figure", "3"], ["architecture", "--peer", "0,9"],
+                                 ["architecture", "--figure", "5"], ["architecture", "--peer", "0,9"],
                                  ["hash", "--wait-timeout", "-1"], ["histogram", "--output-dir", ""]])
 def test_option_errors_exit_2(bad):
     rc, out, err = call(*bad)

@@ -2,7 +2,7 @@
 """Benchmark of the XCD-domain kernels on one MI355X.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--cold] [--only]
-                [--modes aware,oblivious,rotated] [--no-cpu] [--detail FILE]
+                [--modes aware,oblivious,rotated] [--no-cpu] [--no-verify] [--detail FILE]
 
 A step is one pass of the hot path over one batch of synthetic input already resident in
 HBM: one GEMV call, one histogram of 2^28 keys, one hash clear + insert + lookup, one BFS.
@@ -40,11 +40,28 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "GEMV GB/s (% HBM peak); hist Gkeys/s; XCD-aware vs oblivious speedup"
 MODES = ("oblivious", "aware", "rotated")
 
-# HBM bytes per launch of each configuration's roofline kernel, XCD-aware mode: rocprofv3
-# --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch) of that kernel under the same bench
-# command, FETCH_SIZE scaled by the copy-kernel calibration factor (a 256 MiB copy reads
-# 2.000x what FETCH_SIZE counts). Sources: profiles/*_traffic.md.
-TRAFFIC = {}
+# Bytes per step that the roofline kernel(s) move between the L2s and memory (HBM or the
+# Infinity Cache), XCD-aware mode: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB per
+# dispatch) under `bench.py --only --no-cpu --no-verify --steps 10 --warmup 2 --workload W
+# --modes aware [--cold]`, FETCH_SIZE scaled by the copy-kernel calibration factor (a 256 MiB
+# copy reads 2.000x what FETCH_SIZE counts, WRITE_SIZE 1.000x), summed over a step's
+# launches. Atomic and random-access kernels move whole requests (a 16-byte CAS or probe
+# costs a request each way). Source: profiles/traffic_by_config.md.
+TRAFFIC = {
+    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1613981945,
+    ("hash_2p26_lf0.5_u64", "warm", "aware"): 19962486454,
+    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 537631607,
+    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 537631497,
+    ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245587489,
+    ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3925728225,
+    ("bfs_rmat22_ef16", "warm", "aware"): 232832902,
+    ("gemv_f32_4096x4096", "warm", "aware"): 67728407,
+    ("gemv_f32_4096x4096", "cold", "aware"): 67726960,
+    ("gemv_f16_14336x4096", "warm", "aware"): 117662518,
+    ("gemv_f16_14336x4096", "cold", "aware"): 117663801,
+    ("gemv_f16_4096x14336", "warm", "aware"): 118194240,
+    ("gemv_f16_4096x14336", "cold", "aware"): 118199809,
+}
 
 
 def cpu_threads() -> int:
@@ -602,9 +619,11 @@ def kernel_times(wl, mode, steps, flusher=None):
 
 def ic_peak(wl, steps):
     """Best warm read-stream throughput (GB/s) over the workload's own footprint, after one
-    untimed pass: a sweep of chunk order (aware, oblivious), workgroups and loads in flight.
-    The Infinity-Cache roofline of a warm run of that footprint."""
+    untimed pass: a sweep of chunk order (aware, oblivious), workgroups and loads in flight,
+    each point from the read kernel's own dispatch-stamped durations (as the roofline
+    kernels are timed). The Infinity-Cache roofline of a warm run of that footprint."""
     import torch
+    from l2domain_amd import _lib
     from l2domain_amd.domain import home_map, read_stream
     buf = wl.roof_footprint()
     home = getattr(wl, "home", None)
@@ -612,29 +631,28 @@ def ic_peak(wl, steps):
         home = home_map(buf.view(torch.uint8))
     nbytes = buf.numel() * buf.element_size()
     res = {}
-    stream = torch.cuda.current_stream()
     for mode in ("oblivious", "aware"):
-        for wgs in (1024, 2048, 4096):
-            for depth in (2, 4, 8):
+        for wgs in (512, 1024, 2048, 4096, 8192):
+            for depth in (1, 2, 4, 8):
                 read_stream(buf, mode, home, wgs, depth)
                 torch.cuda.synchronize()
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
+                _lib.timing_enable(True)
                 for _ in range(steps):
                     read_stream(buf, mode, home, wgs, depth)
-                e1.record(stream)
                 torch.cuda.synchronize()
-                res[f"{mode}/{wgs}/{depth}"] = nbytes / (e0.elapsed_time(e1) / 1e3 / steps) / 1e9
+                t = _lib.timing_read()
+                _lib.timing_enable(False)
+                ms, n = t["read_stream_kernel"]
+                res[f"{mode}/{wgs}/{depth}"] = nbytes / (ms / 1e3 / n) / 1e9
     best = max(res, key=res.get)
     return res[best], {"best": best, **{k: round(v, 1) for k, v in res.items()}}
 
 
-def run_workload(name, steps, warmup, cold=False, modes=MODES, cpu=True, cpu_budget=2.0):
+def run_workload(name, steps, warmup, cold=False, modes=MODES, cpu=True, cpu_budget=2.0, verify=True):
     import torch
     from l2domain_amd.domain import CacheFlusher
     wl = WORKLOADS[name]()
-    ok = wl.verify()
+    ok = wl.verify() if verify else None
     flusher = CacheFlusher() if cold else None
     sec = {m: time_steps(wl, m, steps, warmup, flusher) for m in modes}
     torch.cuda.synchronize()
@@ -722,6 +740,8 @@ def main():
     ap.add_argument("--modes", default=",".join(MODES), help="comma list of modes to time (default: all three)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--detail", default=None, help="write per-kernel, per-mode detail to this JSON file")
+    ap.add_argument("--no-verify", action="store_true",
+                    help="skip the oracle check (profiling runs only; the line then says verified: null)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -741,7 +761,7 @@ def main():
     from l2domain_amd.domain import topology
 
     r = run_workload(args.workload, args.steps, args.warmup, cold=args.cold, modes=modes, cpu=not args.no_cpu,
-                     cpu_budget=10.0)
+                     cpu_budget=10.0, verify=not args.no_verify)
     wl = r["workload"]
     head = "aware" if "aware" in modes else modes[0]
     sec = r["tput_s"][head]
@@ -778,7 +798,7 @@ def main():
             key = f"{name}_{'cold' if cold else 'warm'}"
             print(f"bench: {key}", file=sys.stderr, flush=True)
             e = run_workload(name, esteps, min(args.warmup, 5), cold=cold, modes=modes,
-                             cpu=not args.no_cpu and not cold)
+                             cpu=not args.no_cpu and not cold, verify=not args.no_verify)
             configs[key] = compact(e, cold)
             details[key] = detail(e, cold)
             del e

@@ -115,6 +115,10 @@ constexpr int kStreamThreads = 256;
 template <int kStreamPairsInFlight>
 __global__ void __launch_bounds__(kStreamThreads)
 read_stream_kernel(const u32x4 *buf, uint64_t nvec, uint64_t npairs, int mode, HomeMap home) {
+    __shared__ uint8_t lattr[2048];  // the buffer's home map (buffers up to 4 GiB)
+    const StagedHome hs = stage_home_nosync(home, reinterpret_cast<uint64_t>(buf), nvec * 16, lattr, 2048,
+                                            mode != XD_MODE_OBLIVIOUS && npairs != 0);
+    __syncthreads();
     uint32_t acc = 0;
     if (mode == XD_MODE_OBLIVIOUS || npairs == 0) {
         const uint64_t stride = (uint64_t)gridDim.x * kStreamThreads;
@@ -141,7 +145,7 @@ read_stream_kernel(const u32x4 *buf, uint64_t nvec, uint64_t npairs, int mode, H
             for (int k = 0; k < kStreamPairsInFlight; ++k) {
                 uint64_t p = p0 + (uint64_t)k * per_die;
                 p = p < npairs ? p : npairs - 1;  // past the end: re-read the last pair
-                const uint64_t c = 2 * p + (home(base + 2 * p * kHomeChunk) ^ want);
+                const uint64_t c = 2 * p + (hs(base + 2 * p * kHomeChunk) ^ want);
                 v[2 * k] = buf[c * kChunkVec + threadIdx.x];
                 v[2 * k + 1] = buf[c * kChunkVec + kStreamThreads + threadIdx.x];
             }

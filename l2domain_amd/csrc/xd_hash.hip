@@ -78,23 +78,12 @@ __device__ __forceinline__ Walk make_walk(int mode) {
 // pages), so the ownership test of the home modes costs no global load.
 constexpr int kLdsPages = 4096;  // tables up to 8 GiB; larger ones read the map from memory
 
-struct SlotHome {
-    const uint8_t *lds;  // staged page map, or nullptr
-    HomeMap g;
-    __device__ __forceinline__ uint32_t operator()(uint64_t addr) const {
-        return lds ? (uint32_t)(((addr >> 13) & 1u) ^ lds[(addr / kHomePage) - g.page0]) : g(addr);
-    }
-};
+typedef StagedHome SlotHome;
 
 // Stages the page map of [base, base + bytes) into `lds` when it fits; every thread calls it.
 __device__ __forceinline__ SlotHome stage_home(const HomeMap &h, uint64_t base, uint64_t bytes, uint8_t *lds,
                                                bool filter) {
-    SlotHome sh{nullptr, h};
-    const uint64_t pages = (base + bytes - 1) / kHomePage - h.page0 + 1;
-    if (filter && h.attr && pages <= (uint64_t)kLdsPages) {
-        for (uint64_t p = threadIdx.x; p < pages; p += blockDim.x) lds[p] = h.attr[p];
-        sh.lds = lds;
-    }
+    const SlotHome sh = stage_home_nosync(h, base, bytes, lds, kLdsPages, filter);
     __syncthreads();
     return sh;
 }

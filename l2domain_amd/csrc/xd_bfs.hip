@@ -28,11 +28,14 @@
 //     on that die (xd_home_map of col), so the neighbour lists are read from the near die;
 //     rotated hands each die the far blocks.
 //   direction: top-down -> bottom-up when m_f > m_u / 14, bottom-up -> top-down when
-//     n_f < V / 24 (Beamer, Asanovic, Patterson, SC'12), decided on the device by a
-//     one-workgroup control kernel after every level. The host enqueues levels in batches
-//     (level, hub expansion, control) of six, then four, and reads the control
-//     block once per batch; the
-//     kernels of levels enqueued after the search ended return at once.
+//     n_f < V / 24 (Beamer, Asanovic, Patterson, SC'12). No control kernel runs between
+//     levels: every workgroup adds its level totals to that level's accumulator (two
+//     memory-side atomics), and every workgroup of the next level recomputes the decision
+//     itself from the previous control state and that accumulator (the same few scalar
+//     steps everywhere, so all agree); workgroup 0 publishes the new state into the other of
+//     two buffers. The host enqueues levels in batches (level, hub expansion) of six, then
+//     four, and replays the same step on the copied state once per batch; the kernels of
+//     levels enqueued after the search ended return at once.
 #include <hip/hip_runtime.h>
 
 #include <string.h>
@@ -54,24 +57,64 @@ constexpr int kLevelBatch = 4;      // levels enqueued per later round trip
 constexpr int kTdWords = 4;         // frontier words a wave loads at once in a top-down level
 constexpr int kTopDown = 0, kBottomUp = 1, kDone = 2;
 
+// S_j: the control state after j completed levels.
 struct BfsCtl {
-    int32_t dir;    // kTopDown, kBottomUp or kDone
-    int32_t depth;  // completed levels; the running level writes depth + 1
+    int32_t dir;    // direction of level j + 1: kTopDown, kBottomUp or kDone
+    int32_t depth;  // completed levels
     int32_t td_steps, bu_steps;
     long long n_f;  // frontier vertices
     long long m_f;  // frontier edges
     long long m_u;  // edges of unvisited vertices
     long long reached_v, reached_e;
-    unsigned long long big_count;  // hub vertices deferred to the grid-wide expansion
 };
 
-struct BfsPartial {  // per workgroup, summed by the control kernel
-    unsigned long long verts;
-    unsigned long long edges;
+// Totals of one level, accumulated by every workgroup of its level and hub kernels into
+// kAccSlots slots of their own 128-byte line (workgroup b adds into slot b mod kAccSlots):
+// thousands of same-address memory-side atomics would serialise at the line's atomic unit.
+constexpr int kAccSlots = 64;
+struct alignas(128) BfsAccSlot {
+    unsigned long long verts, edges;
+    unsigned long long pad[14];
 };
+struct BfsAcc {
+    BfsAccSlot slot[kAccSlots];
+    unsigned long long big;  // hub vertices the level deferred to the grid-wide expansion
+    unsigned long long pad[15];
+};
+
+// S_j lives in s[j % 2] (level j + 1 reads it: level L publishes S_{L-1}); level L
+// accumulates into acc[L % 3] and clears acc[(L + 1) % 3] for the level after it.
+struct BfsCtlBlock {
+    BfsCtl s[2];
+    BfsAcc acc[3];
+};
+
+// S_{j+1} from S_j and level j + 1's totals (the host replays the same step).
+__host__ __device__ inline BfsCtl ctl_step(BfsCtl c, unsigned long long v, unsigned long long e, int32_t V) {
+    if (c.dir == kDone) return c;
+    const int dir = c.dir;
+    if (dir == kTopDown) ++c.td_steps;
+    else ++c.bu_steps;
+    c.depth += 1;
+    c.n_f = (long long)v;
+    c.m_f = (long long)e;
+    if (v == 0) {
+        c.dir = kDone;
+        return c;
+    }
+    c.reached_v += (long long)v;
+    c.reached_e += (long long)e;
+    c.m_u -= (long long)e;
+    if (dir == kTopDown) {
+        if ((double)c.m_f > (double)c.m_u / kAlpha) c.dir = kBottomUp;
+    } else if ((double)c.n_f < (double)V / kBeta) {
+        c.dir = kTopDown;
+    }
+    return c;
+}
 
 struct BfsLayout {
-    size_t visited, front[3], big, ctl, partials, route, total;
+    size_t visited, front[3], big, ctl, route, total;
     int64_t words, nblocks;
 };
 
@@ -88,9 +131,7 @@ static BfsLayout bfs_layout(int32_t V, int64_t nnz) {
     L.nblocks = ((int64_t)V + 63) / 64;
     size_t o = 0;
     L.ctl = o;
-    o = a256(o + sizeof(BfsCtl));
-    L.partials = o;
-    o = a256(o + sizeof(BfsPartial) * kBfsGrid);
+    o = a256(o + sizeof(BfsCtlBlock));
     L.visited = o;
     o = a256(o + 8 * (size_t)L.words);
     for (int i = 0; i < 3; ++i) {
@@ -115,8 +156,7 @@ struct BfsState {
     unsigned long long *visited;
     unsigned long long *front[3];
     int32_t *big;
-    BfsCtl *ctl;
-    BfsPartial *parts;
+    BfsCtlBlock *ctl;
 };
 
 __device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
@@ -166,7 +206,51 @@ __global__ void __launch_bounds__(256) bfs_init_kernel(BfsState st, int32_t src,
         c.m_u = nnz - deg;
         c.reached_v = 1;
         c.reached_e = deg;
-        *st.ctl = c;
+        st.ctl->s[0] = c;
+    }
+    // the accumulators of levels 1 and 2 (level L clears the one of level L + 1 from then on)
+    if (t0 < 2 * kAccSlots) {
+        BfsAccSlot &a = st.ctl->acc[1 + t0 / kAccSlots].slot[t0 % kAccSlots];
+        a.verts = 0ull;
+        a.edges = 0ull;
+    }
+    if (t0 < 3) st.ctl->acc[t0].big = 0ull;
+}
+
+// The control state of level L (S_{L-1}) as every workgroup of the level derives it: the
+// first wave sums level L - 1's slots; workgroup 0 publishes the state for level L + 1 and
+// clears the accumulator of level L + 1. Returns the direction of level L.
+__device__ __forceinline__ int level_dir(const BfsState &st, int L) {
+    __shared__ int sdir;
+    if (threadIdx.x < kWave) {
+        BfsCtl c = st.ctl->s[(L - 1) % 2];
+        if (L >= 2) {
+            const BfsAccSlot &a = st.ctl->acc[(L - 1) % 3].slot[threadIdx.x % kAccSlots];
+            unsigned long long v = threadIdx.x < kAccSlots ? a.verts : 0ull;
+            unsigned long long e = threadIdx.x < kAccSlots ? a.edges : 0ull;
+            v = wave_sum_u64(v);
+            e = wave_sum_u64(e);
+            c = ctl_step(st.ctl->s[L % 2], v, e, st.V);  // S_{L-2} and level L - 1's totals
+            if (blockIdx.x == 0 && threadIdx.x == 0) st.ctl->s[(L - 1) % 2] = c;
+        }
+        if (threadIdx.x == 0) sdir = c.dir;
+    }
+    if (blockIdx.x == 0 && threadIdx.x < kAccSlots) {
+        BfsAccSlot &n = st.ctl->acc[(L + 1) % 3].slot[threadIdx.x];
+        n.verts = 0ull;
+        n.edges = 0ull;
+        if (threadIdx.x == 0) st.ctl->acc[(L + 1) % 3].big = 0ull;
+    }
+    __syncthreads();
+    return sdir;
+}
+
+// Adds a workgroup's level totals (thread 0 holds them after block_sum2).
+__device__ __forceinline__ void add_totals(const BfsState &st, int L, unsigned long long v, unsigned long long e) {
+    if (threadIdx.x == 0) {
+        BfsAccSlot &a = st.ctl->acc[L % 3].slot[blockIdx.x % kAccSlots];
+        if (v) atomicAdd(&a.verts, v);
+        if (e) atomicAdd(&a.edges, e);
     }
 }
 
@@ -318,15 +402,14 @@ __device__ __forceinline__ void bu_blocks(const BfsState &st, int32_t v0a, int32
 
 // One level in the direction the control block names.
 __global__ void __launch_bounds__(kBfsThreads)
-bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const unsigned long long *__restrict__ bcount,
-                 int64_t nblocks) {
-    const int dir = st.ctl->dir;
+bfs_level_kernel(BfsState st, int L, int mode, const int32_t *__restrict__ blist,
+                 const unsigned long long *__restrict__ bcount, int64_t nblocks) {
+    const int dir = level_dir(st, L);
     if (dir == kDone) return;
-    const int depth = st.ctl->depth;
-    const uint32_t lvl = (uint32_t)depth + 1;
-    const unsigned long long *cur_bits = st.front[depth % 3];
-    unsigned long long *next_bits = st.front[(depth + 1) % 3];
-    unsigned long long *later_bits = st.front[(depth + 2) % 3];
+    const uint32_t lvl = (uint32_t)L;
+    const unsigned long long *cur_bits = st.front[(L - 1) % 3];
+    unsigned long long *next_bits = st.front[L % 3];
+    unsigned long long *later_bits = st.front[(L + 1) % 3];
     const int64_t tstride = (int64_t)gridDim.x * blockDim.x;
     const int64_t tid0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (int64_t w = tid0; w < st.words; w += tstride) later_bits[w] = 0ull;  // filled by the next level
@@ -353,7 +436,7 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
                 const int32_t beg = st.rowptr[u];
                 int32_t end = st.rowptr[u + 1];
                 if (end - beg > kBigDeg) {  // a hub: expanded by the whole grid in bfs_hubs_kernel
-                    const unsigned long long slot = atomicAdd(&st.ctl->big_count, 1ull);
+                    const unsigned long long slot = atomicAdd(&st.ctl->acc[L % 3].big, 1ull);
                     st.big[slot] = u;
                     end = beg;
                 }
@@ -389,20 +472,17 @@ bfs_level_kernel(BfsState st, int mode, const int32_t *__restrict__ blist, const
         }
     }
     block_sum2(my_verts, my_edges);
-    if (threadIdx.x == 0) {
-        st.parts[blockIdx.x].verts = my_verts;
-        st.parts[blockIdx.x].edges = my_edges;
-    }
+    add_totals(st, L, my_verts, my_edges);
 }
 
-// Grid-wide expansion of the hub vertices the top-down level deferred.
-__global__ void __launch_bounds__(kBfsThreads) bfs_hubs_kernel(BfsState st) {
-    if (st.ctl->dir != kTopDown) return;
-    const int64_t nbig = (int64_t)st.ctl->big_count;
+// Grid-wide expansion of the hub vertices top-down level L deferred (its state S_{L-1} was
+// published by level L's workgroup 0).
+__global__ void __launch_bounds__(kBfsThreads) bfs_hubs_kernel(BfsState st, int L) {
+    if (st.ctl->s[(L - 1) % 2].dir != kTopDown) return;
+    const int64_t nbig = (int64_t)st.ctl->acc[L % 3].big;
     if (nbig == 0) return;
-    const int depth = st.ctl->depth;
-    const uint32_t lvl = (uint32_t)depth + 1;
-    unsigned long long *next_bits = st.front[(depth + 1) % 3];
+    const uint32_t lvl = (uint32_t)L;
+    unsigned long long *next_bits = st.front[L % 3];
     unsigned long long my_verts = 0, my_edges = 0;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     // every wave takes 64 consecutive list entries at a time (a wave-uniform loop: the runs
@@ -419,43 +499,7 @@ __global__ void __launch_bounds__(kBfsThreads) bfs_hubs_kernel(BfsState st) {
         }
     }
     block_sum2(my_verts, my_edges);
-    if (threadIdx.x == 0) {  // added to the level kernel's partial of the same index
-        st.parts[blockIdx.x].verts += my_verts;
-        st.parts[blockIdx.x].edges += my_edges;
-    }
-}
-
-// End of a level (one workgroup): sums the partials, advances the depth, picks the next
-// direction and clears the per-level counters.
-__global__ void __launch_bounds__(kBfsThreads) bfs_control_kernel(BfsState st, int nparts) {
-    BfsCtl *c = st.ctl;
-    if (c->dir == kDone) return;
-    unsigned long long v = 0, e = 0;
-    for (int i = (int)threadIdx.x; i < nparts; i += kBfsThreads) {
-        v += st.parts[i].verts;
-        e += st.parts[i].edges;
-    }
-    block_sum2(v, e);
-    if (threadIdx.x != 0) return;
-    const int dir = c->dir;
-    if (dir == kTopDown) ++c->td_steps;
-    else ++c->bu_steps;
-    c->depth += 1;
-    c->n_f = (long long)v;
-    c->m_f = (long long)e;
-    c->big_count = 0;
-    if (v == 0) {
-        c->dir = kDone;
-        return;
-    }
-    c->reached_v += (long long)v;
-    c->reached_e += (long long)e;
-    c->m_u -= (long long)e;
-    if (dir == kTopDown) {
-        if ((double)c->m_f > (double)c->m_u / kAlpha) c->dir = kBottomUp;
-    } else if ((double)c->n_f < (double)st.V / kBeta) {
-        c->dir = kTopDown;
-    }
+    add_totals(st, L, my_verts, my_edges);
 }
 
 // Sorts the 64-vertex blocks by the I/O die that homes the start of their adjacency (the
@@ -567,8 +611,7 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     st.visited = reinterpret_cast<unsigned long long *>(ws + L.visited);
     for (int i = 0; i < 3; ++i) st.front[i] = reinterpret_cast<unsigned long long *>(ws + L.front[i]);
     st.big = reinterpret_cast<int32_t *>(ws + L.big);
-    st.ctl = reinterpret_cast<BfsCtl *>(ws + L.ctl);
-    st.parts = reinterpret_cast<BfsPartial *>(ws + L.partials);
+    st.ctl = reinterpret_cast<BfsCtlBlock *>(ws + L.ctl);
     const int bmode = nnz > 0 ? mode : XD_MODE_OBLIVIOUS;  // no adjacency to route by
     const unsigned g256 = (unsigned)std::min<int64_t>(8192, ((int64_t)V + 255) / 256 + 1);
     const void *rt = route;
@@ -584,19 +627,26 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     const auto *blist =
         rt ? reinterpret_cast<const int32_t *>(static_cast<const char *>(rt) + kRouteHeader) : nullptr;
     BfsCtl h{};
+    static thread_local BfsCtlBlock hb;  // 25 KiB: off the stack
     for (int64_t enq = 0;;) {
         const int batch = enq == 0 ? kFirstBatch : kLevelBatch;
         for (int k = 0; k < batch; ++k, ++enq) {
-            {
-                launch("bfs_level_kernel", bfs_level_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, st, bmode, blist, bcount,
-                                   L.nblocks);
-            }
-            launch("bfs_hubs_kernel", bfs_hubs_kernel, dim3(kBigGrid), dim3(kBfsThreads), 0, s, st);
-            launch("bfs_control_kernel", bfs_control_kernel, dim3(1), dim3(kBfsThreads), 0, s, st, kBfsGrid);
+            const int lv = (int)(enq + 1);
+            launch("bfs_level_kernel", bfs_level_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, st, lv, bmode, blist,
+                   bcount, L.nblocks);
+            launch("bfs_hubs_kernel", bfs_hubs_kernel, dim3(kBigGrid), dim3(kBfsThreads), 0, s, st, lv);
             if (int rc = launch_status("bfs level kernels")) return rc;
         }
-        XD_HIP(hipMemcpyAsync(&h, st.ctl, sizeof(h), hipMemcpyDeviceToHost, s));
+        XD_HIP(hipMemcpyAsync(&hb, st.ctl, sizeof(hb), hipMemcpyDeviceToHost, s));
         XD_HIP(hipStreamSynchronize(s));
+        // S_{lv-1} was published by the last level kernel; the step adds that level's totals
+        const int lv = (int)enq;
+        unsigned long long tv = 0, te = 0;
+        for (int i = 0; i < kAccSlots; ++i) {
+            tv += hb.acc[lv % 3].slot[i].verts;
+            te += hb.acc[lv % 3].slot[i].edges;
+        }
+        h = ctl_step(hb.s[(lv - 1) % 2], tv, te, V);
         if (h.dir == kDone) break;
         if (enq > (int64_t)V + 1) return fail(XD_ERR_INCOMPLETE, "xd_bfs_csr: search did not finish");
     }

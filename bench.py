@@ -533,7 +533,7 @@ class Bfs(Workload):
         return ok
 
     def roof_kernels(self, mode):
-        return ("bfs_init_kernel", "bfs_level_kernel", "bfs_hubs_kernel", "bfs_control_kernel")
+        return ("bfs_init_kernel", "bfs_level_kernel", "bfs_hubs_kernel")
 
     def config(self):
         return {"workload": self.name, "vertices": self.g.V, "nnz": self.g.nnz, "source": 0, "seed": 8201,

@@ -67,3 +67,34 @@ def test_gemv_rejects_k_beyond_lds():
     buf = (C.c_float * 64)()
     p = C.addressof(buf)
     assert _lib.lib.xd_gemv_f32(p, p, p, 4, 4 * 4097 * 4, 1, None, None, 0, None) == _lib.XD_ERR_UNSUPPORTED
+
+
+def test_probes_reject_bad_arguments():
+    """The channel probe and the DomainScan latency curves validate before any HIP call."""
+    from l2domain_amd import _lib
+    p = 1 << 21  # a 2 MiB-aligned stand-in address: never dereferenced on these paths
+    us = C.c_float(0.0)
+    vecs = (C.c_uint64 * 6)(*([128] * 6))
+    bad = (C.c_uint64 * 6)(*([128] * 5 + [100]))  # not a multiple of 128
+    E = _lib.XD_ERR_INVALID_ARG
+    assert _lib.lib.xd_channel_time(p, 1 << 22, 0, None, 256, C.byref(us), None) == E
+    assert _lib.lib.xd_channel_time(p, 1 << 22, 0, bad, 256, C.byref(us), None) == E
+    assert _lib.lib.xd_channel_time(p, 1 << 22, 8, vecs, 256, C.byref(us), None) == E     # no XCD 8
+    assert _lib.lib.xd_channel_time(p, 1 << 22, 0, vecs, 6, C.byref(us), None) == E       # iters % 4
+    assert _lib.lib.xd_channel_time(p, 64, 0, vecs, 256, C.byref(us), None) == E          # span > bytes
+    win = (C.c_float * 16)()
+    fast = C.c_float(0.0)
+    masks = (C.c_uint64 * 4)()
+    curves = (C.c_float * 64)()
+    nm = C.c_int(0)
+    args = (win, C.byref(fast), masks, curves, C.byref(nm), None)
+    assert _lib.lib.xd_channel_probe(p, 1 << 23, 0, 6, 20, 256, 64, *args) == E           # bit0 < 7
+    assert _lib.lib.xd_channel_probe(p, 1 << 23, 0, 7, 12, 256, 64, *args) == E           # fewer than 7 bits
+    assert _lib.lib.xd_channel_probe(p, 1 << 23, 0, 7, 20, 256, 0, *args) == E            # max_sets
+    assert _lib.lib.xd_channel_probe(p, 1 << 20, 0, 7, 20, 256, 64, *args) == E           # buffer too small
+    out = (C.c_uint32 * 32)()
+    assert _lib.lib.xd_domain_scan_latency(p, 1 << 10, 7, 31, 0, 0, None, 0, out, None) == E  # 2^31 > bytes
+    assert _lib.lib.xd_domain_scan_latency(p, 1 << 20, 9, 8, 0, 0, None, 0, out, None) == E   # empty range
+    assert _lib.lib.xd_domain_scan_latency(p, 1 << 20, 7, 19, 8, 0, None, 0, out, None) == E  # leader XCD 8
+    assert _lib.lib.xd_domain_scan_latency(p, 1 << 20, 7, 19, 0, 9 << 16, None, 0, out, None) == E  # XCD 9
+    assert _lib.lib.xd_domain_scan_latency(p + 4, 1 << 20, 7, 19, 0, 0, None, 0, out, None) == E    # alignment

@@ -184,6 +184,29 @@ int xd_channel_probe(void *buf, size_t bytes, int xcd, int bit0, int bit1, int i
                      float *out_window_us, float *out_fast_us, uint64_t *out_masks, float *out_curves, int *out_nmasks,
                      void *stream);
 
+/* Memory-side channel probe, the MaskProbe search beyond the L2 (same reference functions as
+ * xd_channel_probe): every workgroup of a 2048-wave grid (all XCDs) adds 1 to the same set of
+ * 64 lines, base + (XOR of vecs[k] over the set bits k of the lane), wave w at dword
+ * (w mod 16) * 8 of each line, `iters` times; a line's returning atomic is served by one
+ * memory-side unit, so the time grows with the largest number of the set's lines sharing one
+ * (it doubles per dimension the set's image loses). The adds change the buffer. base = buf
+ * rounded up to 2 MiB; buf device, bytes must cover the span after the rounding.
+ *
+ * xd_memchannel_time: one query (vecs: 6 host entries, multiples of 128 below 2^40).
+ *
+ * xd_memchannel_probe: over address bits [bit0, bit1] (7 <= bit0, bit0 + 6 <= bit1 < 34, at
+ * most 32 bits), every single bit and every pair of bits x is tried against `nsets` seeded
+ * five-vector sets F: out_ratio[a * nb + b] (a <= b, a == b the single bit, nb = bit1 - bit0
+ * + 1; host, nb * nb floats) = min over the sets of time(F + x) / the fastest time of F's
+ * curve. A ratio near 1 means x spread the set over more units for some F; near 2 or more,
+ * x never changes the unit. *out_inactive: the bits that never do; out_masks[0 .. *out_nmasks)
+ * (host, up to 32): the remaining bits grouped into classes of equal image (pairs that never
+ * change the unit), one XOR mask per class -- the unit-select functions when every bit enters
+ * exactly one of them, which the GPU test checks by predicting random sets. */
+int xd_memchannel_time(void *buf, size_t bytes, const uint64_t *vecs, int iters, float *out_us, void *stream);
+int xd_memchannel_probe(void *buf, size_t bytes, int bit0, int bit1, int iters, int nsets, float *out_ratio,
+                        uint64_t *out_inactive, uint64_t *out_masks, int *out_nmasks, void *stream);
+
 /* Bytes of read traffic xd_cache_flush needs to evict 8 x 4 MB L2 and the 256 MB
  * Infinity Cache (>= 4x their sum). */
 size_t xd_cache_flush_bytes(void);

@@ -84,6 +84,9 @@ SIGNATURES: dict[str, tuple] = {
     "xd_xdom_pchase": (I, [I, I, VP, SZ, I, I, VP, SZ, VP, VP]),
     "xd_mask_probe": (I, [VP, SZ, I, I, I, VP, VP]),
     "xd_domain_scan_latency": (I, [VP, SZ, I, I, I, C.c_uint32, VP, SZ, VP, VP]),
+    "xd_memchannel_time": (I, [VP, SZ, C.POINTER(C.c_uint64), I, C.POINTER(C.c_float), VP]),
+    "xd_memchannel_probe": (I, [VP, SZ, I, I, I, I, C.POINTER(C.c_float), C.POINTER(C.c_uint64),
+                                C.POINTER(C.c_uint64), C.POINTER(C.c_int), VP]),
     "xd_channel_time": (I, [VP, SZ, I, C.POINTER(C.c_uint64), I, C.POINTER(C.c_float), VP]),
     "xd_channel_probe": (I, [VP, SZ, I, I, I, I, I, C.POINTER(C.c_float), C.POINTER(C.c_float),
                              C.POINTER(C.c_uint64), C.POINTER(C.c_float), C.POINTER(C.c_int), VP]),

@@ -233,3 +233,40 @@ def channel_probe(xcd: int = 0, bits=(7, 20), iters: int = 256, max_sets: int = 
     return {"xcd": xcd, "bits": list(range(b0, b1 + 1)), "window_bits": list(range(b0, b0 + nw)),
             "window_us": list(win), "fast_us": float(fast.value), "masks": ms,
             "curves": [list(curves[i * nb:(i + 1) * nb]) for i in range(k)], "active_mask": active}
+
+
+def memchannel_time(vecs, iters: int = 64, device: int = 0) -> float:
+    """One memory-side channel query (xd_memchannel_time): microseconds for 2048 waves on all
+    XCDs to add 1, `iters` times, to the 64 lines base + XOR of the six address vectors `vecs`
+    picked by the lane bits (a distinct dword of each line per wave)."""
+    vecs = [int(x) for x in vecs]
+    assert len(vecs) == 6
+    buf, nbytes = _channel_buffer(max(max(vecs).bit_length() - 1, 7), device)
+    vv = (C.c_uint64 * 6)(*vecs)
+    us = C.c_float(0.0)
+    torch.cuda.synchronize()
+    _lib.call("xd_memchannel_time", ptr(buf), nbytes, vv, iters, C.byref(us), stream_handle())
+    return float(us.value)
+
+
+def memchannel_probe(bits=(7, 20), iters: int = 64, nsets: int = 6, device: int = 0) -> dict:
+    """Memory-side channel probe (xd_memchannel_probe): which address bits select the unit (an
+    Infinity-Cache slice / memory channel) that serves a line's atomics. `ratio[(a, b)]` is the
+    smallest slowdown of a five-vector set when bits a and b (a == b: bit a alone) are added
+    (about 1: they spread the set; about 2 or more: they never change the unit); `inactive` is
+    the mask of bits that never do; `masks` group the other bits into classes of equal effect,
+    one XOR mask per class."""
+    b0, b1 = bits
+    nb = b1 - b0 + 1
+    buf, nbytes = _channel_buffer(b1, device)
+    ratio = (C.c_float * (nb * nb))()
+    inactive = C.c_uint64(0)
+    masks = (C.c_uint64 * 32)()
+    nm = C.c_int(0)
+    torch.cuda.synchronize()
+    _lib.call("xd_memchannel_probe", ptr(buf), nbytes, b0, b1, iters, nsets, ratio, C.byref(inactive), masks,
+              C.byref(nm), stream_handle())
+    k = int(nm.value)
+    return {"bits": list(range(b0, b1 + 1)), "inactive": int(inactive.value),
+            "masks": [int(masks[i]) for i in range(k)],
+            "ratio": {(b0 + a, b0 + b): float(ratio[a * nb + b]) for a in range(nb) for b in range(a, nb)}}

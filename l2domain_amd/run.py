@@ -442,7 +442,8 @@ def run_architecture(args, run, out_dir: Path):
     """architecture/_run_figure.sh for the figures this build measures: 2 (XDom-PChase, the
     leader/follower chase), 3 (DomainScan latency curves of every compute unit after a leader
     on XCD 0) and 4 (MaskProbe, with the L2 channel functions beside it in
-    figure_04_channels.csv); DomainScan's workgroup -> XCD map goes beside every figure."""
+    figure_04_channels.csv and the memory-side unit classes in figure_04_memchannels.csv);
+    DomainScan's workgroup -> XCD map goes beside every figure."""
     tag = "%02d" % args.figure
     data = out_dir / "data"
     csv = data / f"figure_{tag}.csv"
@@ -461,6 +462,11 @@ def run_architecture(args, run, out_dir: Path):
         if not args.dry_run:
             chan.unlink(missing_ok=True)
         st1, _ = run("xd_arch_probe", "chanprobe", 0, 7, 20, f"--csv={chan}")
+        mem = data / "figure_04_memchannels.csv"
+        if not args.dry_run:
+            mem.unlink(missing_ok=True)
+        st3, _ = run("xd_arch_probe", "memprobe", 7, 20, 6, f"--csv={mem}")
+        st1 = st1 or st3
     st2, _ = run("xd_arch_probe", "domainscan", 4096, f"--csv={data / 'domainscan.csv'}")
     if not args.dry_run:
         print(f"Figure {tag} CSV: {csv}")

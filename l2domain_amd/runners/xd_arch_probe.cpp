@@ -8,13 +8,17 @@
 //   xd_arch_probe pchase [leader_xcd=0] [follower_xcd=4] [numel=2048] [stride=128] [--csv=FILE]
 //   xd_arch_probe maskprobe [first_bit=5] [last_bit=29] [reps=8]    [--csv=FILE]
 //   xd_arch_probe chanprobe [xcd=0] [first_bit=7] [last_bit=20]     [--csv=FILE]
+//   xd_arch_probe memprobe [first_bit=7] [last_bit=20] [nsets=6]    [--csv=FILE]
 //
 // scanlat (figure 3): for every compute unit in turn, a flushed-cache leader/follower round
 // (xd_domain_scan_latency) run twice, the second kept; tpc_id = follower index, resource_id =
 // its placement key, tpc_sm0 = its XCD, tpc_sm1 = its rank inside the XCD, follower_sm = its
 // global index XCD * 32 + rank. chanprobe: the L2 channel functions of one XCD as XOR masks;
 // rows per (function, bit) with the time of the bit added to the function's five-bit set
-// (function -1: the windows of six consecutive bits starting at address_bit).
+// (function -1: the windows of six consecutive bits starting at address_bit). memprobe: the
+// memory-side units beyond the L2 (returning atomics from every XCD); one row per bit pair
+// (bit_a == bit_b: the bit alone) with the smallest slowdown it caused, whether it never
+// changes the unit, and the class of equal-effect bits each active bit belongs to.
 //
 // The SM columns of the reference's schemas (leader_sm, follower_sm, sm_a, sm_b) carry XCD
 // ids here: the XCD is the L2 domain on MI355X. pchase flushes every L2 and the Infinity
@@ -36,10 +40,10 @@ int main(int argc, char **argv) {
     Options o(argc, argv);
     const std::string what = o.gets(0, "");
     if (o.help || (what != "domainscan" && what != "scanlat" && what != "pchase" && what != "maskprobe" &&
-                   what != "chanprobe")) {
+                   what != "chanprobe" && what != "memprobe")) {
         printf("usage: %s domainscan [num_wg] | scanlat [first_bit] [last_bit] [leader_xcd] | pchase [leader_xcd] "
                "[follower_xcd] [numel] [stride] | maskprobe [first_bit] [last_bit] [reps] | chanprobe [xcd] "
-               "[first_bit] [last_bit]  [--csv=FILE]\n",
+               "[first_bit] [last_bit] | memprobe [first_bit] [last_bit] [nsets]  [--csv=FILE]\n",
                argv[0]);
         return o.help ? 0 : 2;
     }
@@ -166,6 +170,44 @@ int main(int argc, char **argv) {
         }
         printf("chanprobe xcd=%d bits=%d..%d fast_us=%.1f functions=%d masks=%s active_mask=0x%llx\n", xcd, b0, b1,
                fast, nm, ms.c_str(), (unsigned long long)active);
+        (void)hipFree(buf);
+        return nm > 0 ? 0 : 3;
+    }
+    if (what == "memprobe") {
+        const int b0 = (int)o.geti(1, 7), b1 = (int)o.geti(2, 20), nsets = (int)o.geti(3, 6);
+        if (b0 < 7 || b1 - b0 < 6 || b1 > 33 || b1 - b0 > 31 || nsets < 1 || nsets > 64) return 2;
+        const size_t bytes = (2ull << b1) + (2ull << 20);
+        void *buf;
+        RUN_HIP(hipMalloc(&buf, bytes));
+        RUN_HIP(hipMemset(buf, 0, bytes));
+        const int nb = b1 - b0 + 1;
+        std::vector<float> ratio((size_t)nb * nb);
+        uint64_t inactive = 0, masks[32] = {};
+        int nm = 0;
+        RUN_XD(xd_memchannel_probe(buf, bytes, b0, b1, 64, nsets, ratio.data(), &inactive, masks, &nm, s));
+        auto cls = [&](int bit) {
+            for (int k = 0; k < nm; ++k)
+                if (masks[k] >> bit & 1) return k;
+            return -1;
+        };
+        for (int a = 0; a < nb; ++a)
+            for (int b = a; b < nb; ++b) {
+                const float r = ratio[(size_t)a * nb + b];
+                csv_append(o.csv,
+                           "device_index,device_name,bit_a,bit_b,min_slowdown,never_changes_unit,class_a,class_b,"
+                           "page_stable",
+                           dev + "," + std::to_string(b0 + a) + "," + std::to_string(b0 + b) + "," + std::to_string(r) +
+                               "," + std::to_string((int)(r > 1.4f)) + "," + std::to_string(cls(b0 + a)) + "," +
+                               std::to_string(cls(b0 + b)) + "," + std::to_string((int)(b0 + b <= 20)));
+            }
+        std::string ms;
+        for (int k = 0; k < nm; ++k) {
+            char hx[32];
+            snprintf(hx, sizeof hx, "0x%llx", (unsigned long long)masks[k]);
+            ms += (ms.empty() ? "" : ",") + std::string(hx);
+        }
+        printf("memprobe bits=%d..%d inactive=0x%llx classes=%d masks=%s\n", b0, b1, (unsigned long long)inactive, nm,
+               ms.c_str());
         (void)hipFree(buf);
         return nm > 0 ? 0 : 3;
     }

@@ -98,3 +98,13 @@ def test_probes_reject_bad_arguments():
     assert _lib.lib.xd_domain_scan_latency(p, 1 << 20, 7, 19, 8, 0, None, 0, out, None) == E  # leader XCD 8
     assert _lib.lib.xd_domain_scan_latency(p, 1 << 20, 7, 19, 0, 9 << 16, None, 0, out, None) == E  # XCD 9
     assert _lib.lib.xd_domain_scan_latency(p + 4, 1 << 20, 7, 19, 0, 0, None, 0, out, None) == E    # alignment
+    ratio = (C.c_float * 196)()
+    inactive = C.c_uint64(0)
+    assert _lib.lib.xd_memchannel_time(p, 1 << 22, None, 64, C.byref(us), None) == E
+    assert _lib.lib.xd_memchannel_time(p, 1 << 22, bad, 64, C.byref(us), None) == E
+    assert _lib.lib.xd_memchannel_time(p, 1 << 22, vecs, 0, C.byref(us), None) == E          # iters
+    assert _lib.lib.xd_memchannel_time(p, 64, vecs, 64, C.byref(us), None) == E              # span > bytes
+    margs = (ratio, C.byref(inactive), masks, C.byref(nm), None)
+    assert _lib.lib.xd_memchannel_probe(p, 1 << 23, 6, 20, 64, 6, *margs) == E              # bit0 < 7
+    assert _lib.lib.xd_memchannel_probe(p, 1 << 23, 7, 20, 64, 0, *margs) == E              # nsets
+    assert _lib.lib.xd_memchannel_probe(p, 1 << 20, 7, 20, 64, 6, *margs) == E              # too small

@@ -40,7 +40,7 @@ def test_architecture_figure_2(tmp_path):
 
 def test_architecture_figures_3_and_4(tmp_path):
     """Figure 3: the reference's DomainScan schema, one curve of 25 bits per compute unit;
-    figure 4: MaskProbe rows plus the L2 channel functions beside them."""
+    figure 4: MaskProbe rows plus the L2 channel functions and the memory-side unit classes."""
     for fig in ("3", "4"):
         r = subprocess.run([sys.executable, "-m", "l2domain_amd.run", "architecture", "--figure", fig, "--device", "0",
                             "--output-dir", str(tmp_path)], capture_output=True, text=True, cwd=ROOT, timeout=600)
@@ -52,3 +52,5 @@ def test_architecture_figures_3_and_4(tmp_path):
     chan = (tmp_path / "data" / "figure_04_channels.csv").read_text().splitlines()
     assert chan[0].startswith("device_index,device_name,xcd,function,mask,address_bit")
     assert len(chan) == 1 + 9 + 4 * 14   # 9 windows over bits 7..20, 4 functions of 14 bits
+    mem = (tmp_path / "data" / "figure_04_memchannels.csv").read_text().splitlines()
+    assert mem[0].startswith("device_index,device_name,bit_a,bit_b,min_slowdown") and len(mem) == 1 + 14 * 15 // 2

@@ -451,22 +451,22 @@ bfs_level_kernel(BfsState st, int L, int mode, const int32_t *__restrict__ blist
                       next_bits, lvl, my_verts, my_edges);
         }
     } else {
-        // The XCDs of a die walk that die's block list (aware) or the other die's (rotated),
-        // so the neighbour lists are read from the near (far) die; XCD q of the die owns the
-        // contiguous quarter q of the list in every level, and each of its waves takes two
-        // consecutive list entries, so that the rowptr, level and visited lines of a vertex
-        // range are touched by one XCD only and stay in its L2 from level to level.
+        // The waves of a die walk that die's block list (aware) or the other die's (rotated),
+        // so the neighbour lists are read from the near (far) die; each wave takes two
+        // consecutive list entries and the die's waves interleave over the whole list, as the
+        // oblivious walk interleaves over all blocks. (Giving each XCD of the die a contiguous
+        // quarter instead, so that a vertex range's lines stay in one L2 from level to level,
+        // measured slower: the heavy first bottom-up level took 33.6 against 31.3 us.)
         const int b = (int)blockIdx.x;
         const uint32_t die = wg_die(b);
         const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
         const int32_t *mine = blist + (int64_t)want * nblocks;
         const int64_t cnt = (int64_t)bcount[want];
-        const int q = b % (kNumXcd / 2);  // XCD of the die
-        const int64_t lo = cnt * q / (kNumXcd / 2), hi = cnt * (q + 1) / (kNumXcd / 2);
-        const int64_t wx = (int64_t)(b / kNumXcd) * kWavesPerWg + wave;  // wave of the XCD
-        const int64_t xstride = 2 * (int64_t)(gridDim.x / kNumXcd) * kWavesPerWg;
-        for (int64_t i = lo + 2 * wx; i < hi; i += xstride) {
-            const bool hasb = i + 1 < hi;
+        const int64_t rank = (int64_t)(b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
+        const int64_t wd = rank * kWavesPerWg + wave;  // wave of the die
+        const int64_t xstride = 2 * (int64_t)(gridDim.x / 2) * kWavesPerWg;
+        for (int64_t i = 2 * wd; i < cnt; i += xstride) {
+            const bool hasb = i + 1 < cnt;
             bu_blocks(st, mine[i] * kWave, mine[hasb ? i + 1 : i] * kWave, hasb, cur_bits, next_bits, lvl, my_verts,
                       my_edges);
         }
@@ -506,7 +506,7 @@ __global__ void __launch_bounds__(kBfsThreads) bfs_hubs_kernel(BfsState st, int 
 // block's first vertex on): list[d * nblocks + i] is the i-th block of die d, in ascending
 // block order. The assignment depends only on the graph and the page map, so it is built
 // once per graph (one workgroup walks the blocks in order, 1024 at a time); the bottom-up
-// steps of the home modes give each XCD of a die a contiguous quarter of its die's list.
+// steps of the home modes interleave the waves of a die over its list.
 constexpr int kBlkThreads = 1024;
 __global__ void __launch_bounds__(kBlkThreads)
 bfs_blocks_kernel(const int32_t *__restrict__ rowptr, int64_t nblocks, uint64_t cbase, int64_t col_bytes,

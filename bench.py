@@ -46,7 +46,7 @@ MODES = ("oblivious", "aware", "rotated")
 # --modes aware [--cold]`, FETCH_SIZE scaled by the copy-kernel calibration factor (a 256 MiB
 # copy reads 2.000x what FETCH_SIZE counts, WRITE_SIZE 1.000x), summed over a step's
 # launches. Atomic and random-access kernels move whole requests (a 16-byte CAS or probe
-# costs a request each way). Source: profiles/traffic_by_config.md.
+# costs a request each way).
 TRAFFIC = {
     ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1613981945,
     ("hash_2p26_lf0.5_u64", "warm", "aware"): 19962486454,

@@ -219,9 +219,12 @@ __global__ void __launch_bounds__(256) bfs_init_kernel(BfsState st, int32_t src,
 
 // The control state of level L (S_{L-1}) as every workgroup of the level derives it: the
 // first wave sums level L - 1's slots; workgroup 0 publishes the state for level L + 1 and
-// clears the accumulator of level L + 1. Returns the direction of level L.
-__device__ __forceinline__ int level_dir(const BfsState &st, int L) {
-    __shared__ int sdir;
+// clears the accumulator of level L + 1. Returns the direction of level L; *heavy says
+// whether more than 1/64 of the adjacency is still unvisited (the bottom-up walk of the home
+// modes routes by home only then: in the sparse levels after that, nearly every block is
+// already visited, so a wave's cost is its per-block loads, not the adjacency stream).
+__device__ __forceinline__ int level_dir(const BfsState &st, int L, bool *heavy) {
+    __shared__ int sdir, sheavy;
     if (threadIdx.x < kWave) {
         BfsCtl c = st.ctl->s[(L - 1) % 2];
         if (L >= 2) {
@@ -233,7 +236,10 @@ __device__ __forceinline__ int level_dir(const BfsState &st, int L) {
             c = ctl_step(st.ctl->s[L % 2], v, e, st.V);  // S_{L-2} and level L - 1's totals
             if (blockIdx.x == 0 && threadIdx.x == 0) st.ctl->s[(L - 1) % 2] = c;
         }
-        if (threadIdx.x == 0) sdir = c.dir;
+        if (threadIdx.x == 0) {
+            sdir = c.dir;
+            sheavy = c.m_u > (c.m_u + c.reached_e) / 64;
+        }
     }
     if (blockIdx.x == 0 && threadIdx.x < kAccSlots) {
         BfsAccSlot &n = st.ctl->acc[(L + 1) % 3].slot[threadIdx.x];
@@ -242,6 +248,7 @@ __device__ __forceinline__ int level_dir(const BfsState &st, int L) {
         if (threadIdx.x == 0) st.ctl->acc[(L + 1) % 3].big = 0ull;
     }
     __syncthreads();
+    *heavy = sheavy != 0;
     return sdir;
 }
 
@@ -404,7 +411,8 @@ __device__ __forceinline__ void bu_blocks(const BfsState &st, int32_t v0a, int32
 __global__ void __launch_bounds__(kBfsThreads)
 bfs_level_kernel(BfsState st, int L, int mode, const int32_t *__restrict__ blist,
                  const unsigned long long *__restrict__ bcount, int64_t nblocks) {
-    const int dir = level_dir(st, L);
+    bool heavy = false;
+    const int dir = level_dir(st, L, &heavy);
     if (dir == kDone) return;
     const uint32_t lvl = (uint32_t)L;
     const unsigned long long *cur_bits = st.front[(L - 1) % 3];
@@ -443,7 +451,7 @@ bfs_level_kernel(BfsState st, int L, int mode, const int32_t *__restrict__ blist
                 for (int32_t j = beg; j < end; ++j) td_visit(st, true, st.col[j], lvl, next_bits, my_verts, my_edges);
             }
         }
-    } else if (mode == XD_MODE_OBLIVIOUS) {
+    } else if (mode == XD_MODE_OBLIVIOUS || !heavy) {
         const int64_t bstride = (int64_t)gridDim.x * kWavesPerWg;
         for (int64_t blk = (int64_t)blockIdx.x * kWavesPerWg + wave; blk < nblocks; blk += 2 * bstride) {
             const bool hasb = blk + bstride < nblocks;

@@ -54,7 +54,7 @@ TRAFFIC = {
     ("hist256_bytes_512MiB_mix32", "cold", "aware"): 537631497,
     ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245587489,
     ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3925728225,
-    ("bfs_rmat22_ef16", "warm", "aware"): 232691487,
+    ("bfs_rmat22_ef16", "warm", "aware"): 239009619,
     ("gemv_f32_4096x4096", "warm", "aware"): 67728407,
     ("gemv_f32_4096x4096", "cold", "aware"): 67726960,
     ("gemv_f16_14336x4096", "warm", "aware"): 117662518,

@@ -90,13 +90,17 @@ __device__ __forceinline__ void h8_add_vec(uint32_t *h, uint4 v, uint32_t nv, ui
 // the nvec full vectors of the data, which start at address wbeg (16-byte aligned). ok = the
 // vector lies inside them; otherwise vector 0 is loaded (the load stays unconditional) and
 // must not be counted. Indexing from the kernel's pointer argument keeps the load in the
-// global address space (a flat load would also count against the LDS wait counter).
+// global address space (a flat load would also count against the LDS wait counter). The load
+// is non-temporal: every word is read once (512 MiB: aware 5.43 -> 5.90 TB/s warm, 5.49 ->
+// 6.02 TB/s cold).
 __device__ __forceinline__ uint4 h8_load(const uint4 *__restrict__ words4, uint64_t c, uint64_t wbeg, uint64_t nvec,
                                          int tid, bool &ok) {
     const uint64_t a = c * kH8Chunk + (uint64_t)tid * 16u;
     const uint64_t i = (a - wbeg) / 16u;  // wraps to a huge value below wbeg
     ok = a >= wbeg && i < nvec;
-    return words4[ok ? i : 0];
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(&words4[ok ? i : 0]));
+    return make_uint4(t.x, t.y, t.z, t.w);
 }
 
 __global__ void __launch_bounds__(kH8Threads)

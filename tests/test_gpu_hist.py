@@ -90,8 +90,10 @@ def test_workspace_reuse_shrinking_input():
 
 
 def _hot_case_keys(case: str) -> tuple[np.ndarray, int]:
-    """2^25 keys: more than two tiles per persistent partition workgroup, so every case runs
-    the claim tiles and the read-only-table tiles of the hot-key partition."""
+    """2^25 keys (over a thousand partition tiles) of skewed distributions: hot bins crowding
+    one bucket, one bucket only, one bin per key value, a single key. They load the partition's
+    counter columns unevenly, and the count pass's per-wave votes on its two peeled hot keys
+    keep switching or never switch."""
     n = 1 << 25
     rng = np.random.default_rng(sum(map(ord, case)))
     # (the device generator matches the oracle's key by key: test_device_zipf_keys_match_oracle_generator)

@@ -47,8 +47,8 @@ __global__ void __launch_bounds__(256) hash_init_kernel(Slot *table, uint64_t sl
 // Work walk. Every wave takes 64-item chunks of the input: chunk c = first + k * stride.
 // Oblivious: the chunks of the whole grid in order. Home modes: the waves of each die walk
 // all chunks (each die sees every item) and keep only the items whose home slot lies on the
-// wanted die; the kept item indices are compacted into a per-wave LDS queue and probed 64
-// at a time, so that no lane idles through a probe loop.
+// wanted die; the kept items (index and key) are compacted into a per-wave LDS queue and
+// probed 64 at a time, so that no lane idles through a probe loop.
 struct Walk {
     uint64_t first, stride;  // in 64-item chunks
     uint32_t want;           // die whose items this wave takes (home modes)

@@ -48,10 +48,10 @@ MODES = ("oblivious", "aware", "rotated")
 # launches. Atomic and random-access kernels move whole requests (a 16-byte CAS or probe
 # costs a request each way).
 TRAFFIC = {
-    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1613981945,
+    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1614009616,
     ("hash_2p26_lf0.5_u64", "warm", "aware"): 19962486454,
-    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 537631607,
-    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 537631497,
+    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 545405734,
+    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 545042400,
     ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245587489,
     ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3925728225,
     ("bfs_rmat22_ef16", "warm", "aware"): 239009619,

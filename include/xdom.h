@@ -352,6 +352,22 @@ int xd_hash_init(void *table, uint64_t slots, void *stream);
 int xd_hash_insert_u64(void *table, uint64_t slots, const uint64_t *keys, const uint64_t *vals, uint64_t n,
                        int mode, const uint8_t *home_attr, unsigned long long *failed, void *stream);
 
+/* Bulk build: the table's previous contents are replaced by the n pairs (the insert's
+ * semantics on a freshly cleared table: EMPTY keys skipped, a repeated key keeps one of its
+ * values, pairs that find no slot counted into *failed). No counterpart routine in the
+ * reference, which builds its table serially on the CPU
+ * (applications/hash/src/hash_probe_dep.cu:226-241); this is that build on the GPU. Tables of
+ * 2^15 .. 2^30 slots are built range by range in LDS (4096 slots per range, two split passes,
+ * plain stores, a compare-and-swap fix-up for the few pairs that run past a range's end);
+ * XD_MODE_AWARE makes a range the 8 KiB chunks homed on one I/O die and builds it on that
+ * die, XD_MODE_ROTATED on the other die. Other sizes and n = 0 are cleared and inserted
+ * (xd_hash_init + xd_hash_insert_u64). The workspace (xd_hash_build_workspace_size, 0 for
+ * those shapes; about 3.1 n x 16 bytes otherwise) needs no initial contents. */
+size_t xd_hash_build_workspace_size(uint64_t n, uint64_t slots);
+int xd_hash_build_u64(void *table, uint64_t slots, const uint64_t *keys, const uint64_t *vals, uint64_t n,
+                      int mode, const uint8_t *home_attr, void *workspace, size_t workspace_bytes,
+                      unsigned long long *failed, void *stream);
+
 /* found_out[i] = 1 and vals_out[i] = value if queries[i] is present, else 0 and 0. */
 int xd_hash_lookup_u64(const void *table, uint64_t slots, const uint64_t *queries, uint64_t n,
                        uint64_t *vals_out, uint8_t *found_out, int mode, const uint8_t *home_attr,

@@ -102,6 +102,8 @@ SIGNATURES: dict[str, tuple] = {
     "xd_hash_init": (I, [VP, U64, VP]),
     "xd_hash_insert_u64": (I, [VP, U64, VP, VP, U64, I, VP, VP, VP]),
     "xd_hash_lookup_u64": (I, [VP, U64, VP, U64, VP, VP, I, VP, VP]),
+    "xd_hash_build_workspace_size": (SZ, [U64, U64]),
+    "xd_hash_build_u64": (I, [VP, U64, VP, VP, U64, I, VP, VP, SZ, VP, VP]),
     "xd_gen_hash_kv": (I, [VP, VP, U64, U64, VP]),
     "xd_gen_hash_queries": (I, [VP, U64, U64, U64, U64, VP]),
     "xd_dep_make_keys": (I, [U64, U64, VP, C.c_int32, C.c_int32, VP, VP]),

@@ -19,24 +19,11 @@
 //   rotated:   the swapped control: each die handles the keys homed on the other die.
 #include <hip/hip_runtime.h>
 
-#include "xd_common.hpp"
+#include "xd_hash.hpp"
 
 namespace xd {
 
-constexpr uint64_t kEmpty = ~0ull;
 constexpr int kHashThreads = 256;
-constexpr uint64_t kMaxProbe = 1ull << 16;
-
-struct __attribute__((aligned(16))) Slot {
-    uint64_t key;
-    uint64_t val;
-};
-
-__host__ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
-}
 
 __global__ void __launch_bounds__(256) hash_init_kernel(Slot *table, uint64_t slots) {
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -148,23 +135,7 @@ hash_insert_kernel(Slot *__restrict__ table, uint64_t mask, const uint64_t *__re
     auto keep = [&](uint64_t key) { return sh(base + (mix64(key) & mask) * sizeof(Slot)) == w.want; };
     auto body = [&](uint64_t i, uint64_t key) {
         if (key == kEmpty) return;
-        const uint64_t val = vals[i];
-        uint64_t s = mix64(key) & mask;
-        for (uint64_t step = 0; step < max_probe; ++step) {
-            unsigned long long *kp = reinterpret_cast<unsigned long long *>(&table[s].key);
-            // A slot's key only ever changes from EMPTY to a key, so a plain (possibly stale)
-            // read can only show EMPTY for a taken slot; the compare-and-swap then returns the
-            // real owner. Only slots that look free pay for the memory-side atomic.
-            const uint64_t cur = __hip_atomic_load(kp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            uint64_t owner = cur;
-            if (cur == kEmpty) owner = atomicCAS(kp, (unsigned long long)kEmpty, (unsigned long long)key);
-            if (owner == kEmpty || owner == key) {
-                table[s].val = val;
-                return;
-            }
-            s = (s + 1) & mask;
-        }
-        if (failed) atomicAdd(failed, 1ull);
+        if (!slot_insert(table, mask, mix64(key) & mask, key, vals[i], max_probe) && failed) atomicAdd(failed, 1ull);
     };
     for_each_owned(w, n, filter, qidx[threadIdx.x / kWave], qkey[threadIdx.x / kWave], key_of, keep, body);
 }

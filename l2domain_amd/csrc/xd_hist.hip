@@ -91,19 +91,6 @@ static HistLayout hist_layout(size_t n, uint32_t num_bins) {
     return L;
 }
 
-// Inclusive scan over the wave with DPP (no LDS traffic): row_shr 1, 2, 4, 8 scan each row
-// of 16 lanes (a lane whose source lies before its row adds 0), then row_bcast:15 adds row
-// 0's total to row 1 and row 2's to row 3, and row_bcast:31 adds lane 31's prefix to rows 2-3.
-__device__ __forceinline__ uint32_t wave_incl_scan_u32(uint32_t v) {
-    v += dpp_u32<0x111>(v);
-    v += dpp_u32<0x112>(v);
-    v += dpp_u32<0x114>(v);
-    v += dpp_u32<0x118>(v);
-    v += dpp_u32<0x142, 0xa>(v);
-    v += dpp_u32<0x143, 0xc>(v);
-    return v;
-}
-
 // A 16-byte non-temporal load, for data read exactly once: the partition's key stream and
 // the count pass's runs (at 2^28 keys, aware: partition 272 -> 242 us, count 165 -> 179 us
 // with only the key stream non-temporal, 179 -> 169-179 us with both).

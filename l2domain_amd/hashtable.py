@@ -32,6 +32,7 @@ class HashTable:
         nbytes = int(_lib.lib.xd_hash_table_bytes(self.slots))
         self.table = torch.empty(nbytes // 8, dtype=torch.int64, device=dev)
         self.failed = torch.zeros(1, dtype=torch.int64, device=dev)
+        self._build_ws = None
         self.clear(stream)
         self.home_attr = None
         if map_homes:
@@ -49,6 +50,22 @@ class HashTable:
         _lib.call("xd_hash_insert_u64", ptr(self.table), self.slots, ptr(keys) if n else None,
                   ptr(vals) if n else None, n, mode_id(mode), ptr(self.home_attr), ptr(self.failed),
                   stream_handle(stream))
+
+    def build(self, keys: torch.Tensor, vals: torch.Tensor, mode="aware", stream=None) -> None:
+        """Replaces the table's contents by the pairs (xd_hash_build_u64): the same lookups as
+        clear() followed by insert(). The workspace is kept for later builds of up to as
+        many pairs."""
+        n = keys.numel()
+        if vals.numel() != n or keys.element_size() != 8 or vals.element_size() != 8:
+            raise ValueError("keys and vals must be equal-length 64-bit tensors")
+        need = int(_lib.lib.xd_hash_build_workspace_size(n, self.slots))
+        if need and (self._build_ws is None or self._build_ws.numel() < need):
+            self._build_ws = None
+            self._build_ws = torch.empty(need, dtype=torch.uint8, device=self.table.device)
+        ws = self._build_ws if need else None
+        _lib.call("xd_hash_build_u64", ptr(self.table), self.slots, ptr(keys) if n else None,
+                  ptr(vals) if n else None, n, mode_id(mode), ptr(self.home_attr), ptr(ws),
+                  ws.numel() if ws is not None else 0, ptr(self.failed), stream_handle(stream))
 
     def lookup(self, queries: torch.Tensor, mode="aware", vals_out=None, found_out=None, stream=None):
         n = queries.numel()

@@ -135,3 +135,19 @@ def test_config_2p26_insert_lookup(config_ref, mode):
     np.testing.assert_array_equal(host(v), rv)
     del t
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_config_2p26_build_lookup(config_ref, mode):
+    """The bench's step: the range build (xd_hash_build_u64) of the 2^26 pairs into 2^27
+    slots, then the 2^26 lookups, against the serial build."""
+    keys, vals, q, rv, rf = config_ref
+    t = HashTable(HASH_SLOTS)
+    t.build(keys, vals, mode=mode)
+    v, f = t.lookup(q, mode=mode)
+    torch.cuda.synchronize()
+    assert t.failures() == 0
+    np.testing.assert_array_equal(f.cpu().numpy(), rf)
+    np.testing.assert_array_equal(host(v), rv)
+    del t
+    torch.cuda.empty_cache()

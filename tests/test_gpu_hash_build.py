@@ -1,0 +1,128 @@
+"""Bulk build (xd_hash_build_u64) parity on the GPU: after a build, every lookup answers as
+after the oracle's serial build of the same pairs (HASH.cu:226-241, probe HASH.cu:46-64),
+found/value bit-exact, in every mode; the spill and overflow paths are forced with keys
+crowded into one range."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as ora
+from l2domain_amd.hashtable import EMPTY, HashTable
+
+pytestmark = pytest.mark.gpu
+MODES = ["oblivious", "aware", "rotated"]
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint64).view(np.int64)).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    return t.cpu().numpy().view(np.uint64)
+
+
+def mix64(z: np.ndarray) -> np.ndarray:
+    """splitmix64's output function (the table's slot hash), in wrapping uint64 arithmetic."""
+    z = z.astype(np.uint64)
+    with np.errstate(over="ignore"):
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def check_build(slots, keys, vals, mode, queries, failures=0, table=None):
+    ref = ora.HashTable(slots)
+    assert ref.build(keys, vals) == failures
+    rv, rf = ref.lookup(queries)
+    t = table if table is not None else HashTable(slots)
+    print(f"build slots={slots} n={keys.size} mode={mode}", flush=True)
+    t.build(dev(keys), dev(vals), mode=mode)
+    v, f = t.lookup(dev(queries), mode="oblivious")
+    torch.cuda.synchronize()
+    assert t.failures() == failures
+    got_f, got_v = f.cpu().numpy(), host(v)
+    if failures == 0:
+        np.testing.assert_array_equal(got_f, rf)
+        np.testing.assert_array_equal(got_v, rv)
+    return t, got_f, got_v
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("slots,n", [(8, 5), (1 << 12, 1500), (1 << 15, 16000), (1 << 16, 3 * 4096 + 77),
+                                     (1 << 18, 100000), (1 << 20, 9 * 4096 + 1)])
+def test_build_matches_serial_build(slots, n, mode):
+    """Tables below 2^15 slots take the clear + insert path, the others the range build; load
+    factors from 0.02 to 0.63."""
+    keys, vals = ora.hash_kv(n + 600, slots + 7)
+    q = np.concatenate([keys[:n], keys[n:], keys[: n : 3]])
+    np.random.default_rng(slots).shuffle(q)
+    check_build(slots, keys[:n].copy(), vals[:n].copy(), mode, q)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_build_repeats_empty_and_unaligned(mode):
+    """A key repeated in two tiles (one slot, one of its values), an EMPTY key (skipped), and
+    key/value arrays that start 8 bytes into a 16-byte vector (the per-element load path)."""
+    slots, n = 1 << 16, 20001
+    keys, vals = ora.hash_kv(n + 1, 77)
+    keys = keys.copy()
+    keys[15000] = keys[3]
+    keys[n // 2] = EMPTY
+    kd, vd = dev(keys), dev(vals)  # element 0 is skipped: views at an 8-byte offset
+    assert kd[1:].data_ptr() % 16 == 8
+    ref = ora.HashTable(slots)
+    assert ref.build(keys[1:], vals[1:]) == 0
+    q = keys[1:]
+    rv, rf = ref.lookup(q)
+    t = HashTable(slots)
+    t.build(kd[1:], vd[1:], mode=mode)
+    v, f = t.lookup(dev(q), mode=mode)
+    torch.cuda.synchronize()
+    assert t.failures() == 0
+    got_f, got_v = f.cpu().numpy(), host(v)
+    i3, i15 = 2, 14999  # positions of the repeated key among keys[1:]
+    assert got_f[i3] == 1 and got_v[i3] in (vals[3], vals[15000]) and got_v[i15] == got_v[i3]
+    got_v[i3] = got_v[i15] = rv[i3]
+    np.testing.assert_array_equal(got_f, rf)
+    np.testing.assert_array_equal(got_v, rv)
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("n", [3000, 6000])
+def test_build_crowded_range_spills(n, mode):
+    """n keys whose home slots all lie in the first 4096 of 2^16 slots: the split regions
+    overflow their capacity and the runs spill past their end, so most pairs reach the table
+    through the overflow list and the compare-and-swap fix-up."""
+    slots = 1 << 16
+    cand, cvals = ora.hash_kv(1 << 20, 4242)
+    sel = np.nonzero((mix64(cand) & np.uint64(slots - 1)) < np.uint64(4096))[0][:n]
+    assert sel.size == n
+    keys, vals = cand[sel].copy(), cvals[sel].copy()
+    q = np.concatenate([keys, cand[sel[-1] + 1 : sel[-1] + 2001]])
+    check_build(slots, keys, vals, mode, q)
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_build_replaces_contents_and_empty_batch(mode):
+    slots = 1 << 15
+    a, av = ora.hash_kv(9000, 1)
+    b, bv = ora.hash_kv(9000, 2)
+    t, _, _ = check_build(slots, a, av, mode, a)
+    check_build(slots, b, bv, mode, np.concatenate([a, b]), table=t)  # a's keys are gone
+    t.build(dev(a[:0]), dev(av[:0]), mode=mode)
+    _, f = t.lookup(dev(b), mode=mode)
+    torch.cuda.synchronize()
+    assert int(f.cpu().numpy().sum()) == 0
+
+
+@pytest.mark.parametrize("mode", MODES)
+def test_build_full_table_failures(mode):
+    """2^15 + 50 distinct keys into 2^15 slots: exactly 50 find no slot."""
+    slots = 1 << 15
+    keys, vals = ora.hash_kv(slots + 50, 9)
+    t = HashTable(slots)
+    t.build(dev(keys), dev(vals), mode=mode)
+    _, f = t.lookup(dev(keys), mode=mode)
+    torch.cuda.synchronize()
+    assert t.failures() == 50
+    assert int(f.cpu().numpy().sum()) == slots

@@ -47,9 +47,9 @@ constexpr int kSplitThreads = 1024;
 constexpr int kSplitPer = 4;  // pairs per thread
 constexpr uint32_t kSplitTile = kSplitThreads * kSplitPer;
 constexpr int kMaxDigitBits = 9;
-constexpr int kBuildThreads = 512;
+constexpr int kBuildThreads = 1024;  // 2 workgroups per CU (LDS); 512 threads: build 721 -> 612 us
 constexpr int kBuildPer = kRange / kBuildThreads;  // slots written per thread
-constexpr int kBuildLoad = 8;                       // pairs in flight per thread
+constexpr int kBuildLoad = 4;                       // pairs in flight per thread
 constexpr uint32_t kSpillPerRange = 32;  // expected ~0.25 per run end (two per aware range)
 constexpr int kMinLgSlots = 15;          // 8 ranges: one per XCD slot of a grid
 constexpr int kMaxLgSlots = 30;          // two digits of at most 9 bits
@@ -106,6 +106,14 @@ __device__ __forceinline__ Slot load_pair_nt(const Slot *p) {
 __device__ __forceinline__ void store_pair(Slot *p, const Slot &s) {
     *reinterpret_cast<uint4 *>(p) = make_uint4((uint32_t)s.key, (uint32_t)(s.key >> 32), (uint32_t)s.val,
                                                (uint32_t)(s.val >> 32));
+}
+
+// The table is written once here and read back only by later lookups: non-temporal stores
+// (build kernel 612 -> 589 us at 2^27 slots). The split regions, which the next pass reads,
+// keep ordinary stores (non-temporal ones made each split pass 100 us slower).
+__device__ __forceinline__ void store_pair_nt(Slot *p, const Slot &s) {
+    const u32x4 v = {(uint32_t)s.key, (uint32_t)(s.key >> 32), (uint32_t)s.val, (uint32_t)(s.val >> 32)};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(p));
 }
 
 __device__ __forceinline__ void to_overflow(const SplitDst &d, const Slot &s) {
@@ -287,7 +295,7 @@ hb_build_kernel(BuildGeom g, int mode, const Slot *__restrict__ reg, const uint3
         }
     }
     __syncthreads();
-    // Write-out: pass k stores local chunk k (slots 512 k .. 512 k + 511) as one 8 KiB piece.
+    // Write-out: pass k stores local slots kBuildThreads k .. kBuildThreads (k + 1) - 1, whole 8 KiB chunks.
 #pragma unroll
     for (int k = 0; k < kBuildPer; ++k) {
         const uint32_t j = (uint32_t)tid + (uint32_t)k * kBuildThreads;
@@ -299,7 +307,7 @@ hb_build_kernel(BuildGeom g, int mode, const Slot *__restrict__ reg, const uint3
             const uint32_t he = sh(g.base + even * sizeof(Slot));
             slot = even + (he == (r & 1u) ? 0 : kChunkSlots) + (j & (kChunkSlots - 1));
         }
-        store_pair(&table[slot], tab[j]);
+        store_pair_nt(&table[slot], tab[j]);
     }
     if (tid == 0) spill_cnt[r] = s_nsp;
 }

@@ -49,6 +49,7 @@ MODES = ("oblivious", "aware", "rotated")
 # costs a request each way).
 TRAFFIC = {
     ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1614009616,
+    ("hash_2p26_lf0.5_u64", "warm", "aware"): 20180216301,
     ("hist256_bytes_512MiB_mix32", "warm", "aware"): 545405734,
     ("hist256_bytes_512MiB_mix32", "cold", "aware"): 545042400,
     ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245587489,

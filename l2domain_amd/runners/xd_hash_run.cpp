@@ -176,6 +176,9 @@ static int insert_lookup(const Options &o) {
     }
     RUN_HIP(hipMalloc(&failed, 8));
     RUN_HIP(hipMalloc(&table, xd_hash_table_bytes(C)));
+    const size_t ws_bytes = xd_hash_build_workspace_size(K, C);
+    void *ws = nullptr;
+    if (ws_bytes) RUN_HIP(hipMalloc(&ws, ws_bytes));
     RUN_XD(xd_gen_hash_kv(keys, vals, K, seed, s));
     RUN_XD(xd_gen_hash_queries(q, Q, K, seed, qseed, s));
     HomeMap home(table, xd_hash_table_bytes(C), s);
@@ -223,13 +226,37 @@ static int insert_lookup(const Options &o) {
            (double)K / C, hfail);
     printf("Correctness: %s\n\n", pass ? "PASS" : "FAIL");
 
-    float ins[3] = {0, 0, 0}, look[3] = {0, 0, 0};
+    // the bulk build (xd_hash_build_u64) in place of init + insert: the same lookups
+    auto build = [&](int mode) {
+        return time_ms(s, [&] {
+            RUN_XD(xd_hash_build_u64(table, C, keys, vals, K, mode, home.attr, ws, ws_bytes, failed, s));
+        });
+    };
+    bool bpass = true;
+    for (int mode = 0; mode < 3; ++mode) {
+        build(mode);
+        RUN_XD(xd_hash_lookup_u64(table, C, q, Q, vout[mode], fout[mode], mode, home.attr, s));
+        RUN_HIP(hipStreamSynchronize(s));
+        RUN_HIP(hipMemcpy(gv.data(), vout[mode], Q * 8, hipMemcpyDeviceToHost));
+        RUN_HIP(hipMemcpy(gf.data(), fout[mode], Q, hipMemcpyDeviceToHost));
+        bpass = bpass && gv == ev && gf == ef;
+    }
+    RUN_HIP(hipMemcpy(&hfail, failed, 8, hipMemcpyDeviceToHost));
+    bpass = bpass && hfail == 0;
+    pass = pass && bpass;
+    printf("Build correctness: %s\n", bpass ? "PASS" : "FAIL");
+
+    float ins[3] = {0, 0, 0}, look[3] = {0, 0, 0}, bld[3] = {0, 0, 0};
     for (int r = 0; r < runs; ++r)
-        for (int mode = 0; mode < 3; ++mode) step(mode, &ins[mode], &look[mode]);
+        for (int mode = 0; mode < 3; ++mode) {
+            step(mode, &ins[mode], &look[mode]);
+            bld[mode] += build(mode);
+        }
     double ms[3];
     for (int m = 0; m < 3; ++m) {
         ins[m] /= runs;
         look[m] /= runs;
+        bld[m] /= runs;
         ms[m] = (double)ins[m] + look[m];
     }
     printf("%-28s %8.3f ms\n", "Persistent baseline", ms[0]);
@@ -237,6 +264,7 @@ static int insert_lookup(const Options &o) {
     printf("%-28s %8.3f ms  (speedup %.2fx)\n", "Swapped", ms[2], ms[0] / ms[2]);
     printf("insert_ms baseline=%.6f aware=%.6f swapped=%.6f\n", ins[0], ins[1], ins[2]);
     printf("lookup_ms baseline=%.6f aware=%.6f swapped=%.6f\n", look[0], look[1], look[2]);
+    printf("build_ms baseline=%.6f aware=%.6f swapped=%.6f\n", bld[0], bld[1], bld[2]);
     printf("mops baseline=%.1f aware=%.1f swapped=%.1f\n", (K + Q) / (ms[0] * 1e3), (K + Q) / (ms[1] * 1e3),
            (K + Q) / (ms[2] * 1e3));
     const double lbytes = 33.0 * Q;

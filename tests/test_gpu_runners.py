@@ -92,6 +92,9 @@ def test_hash_runner(tmp_path, workload):
     for key in ("baseline_ms", "aware_ms", "swapped_ms", "aware_speedup", "swapped_speedup"):
         assert float(kv[key]) > 0
     assert (tmp_path / "x.csv").read_text().splitlines()[0].startswith("K,Q,C,effective_load,L,h,H,baseline_ms")
+    if workload == "insert_lookup":  # the bulk build checked and timed beside the insert
+        assert "Build correctness: PASS" in out
+        assert float(first_field(out, "build_ms").split("=")[1]) > 0
 
 
 @pytest.mark.parametrize("args", [(65536, 8, 128, 2, 95, 4096, 1, 8201),  # the reference's quick preset

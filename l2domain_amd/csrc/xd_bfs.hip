@@ -635,7 +635,20 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     const auto *blist =
         rt ? reinterpret_cast<const int32_t *>(static_cast<const char *>(rt) + kRouteHeader) : nullptr;
     BfsCtl h{};
-    static thread_local BfsCtlBlock hb;  // 25 KiB: off the stack
+    // The host copy of the control block (25 KiB) lives in pinned memory, allocated once per
+    // thread: a copy into pageable memory is staged by the runtime and cost ~15 us a search.
+    static thread_local BfsCtlBlock *hb_pinned = nullptr;
+    static thread_local BfsCtlBlock hb_pageable;
+    static thread_local bool hb_tried = false;
+    if (!hb_tried) {
+        hb_tried = true;
+        if (hipHostMalloc(reinterpret_cast<void **>(&hb_pinned), sizeof(BfsCtlBlock), hipHostMallocDefault) !=
+            hipSuccess) {
+            (void)hipGetLastError();
+            hb_pinned = nullptr;
+        }
+    }
+    BfsCtlBlock &hb = hb_pinned ? *hb_pinned : hb_pageable;
     for (int64_t enq = 0;;) {
         const int batch = enq == 0 ? kFirstBatch : kLevelBatch;
         for (int k = 0; k < batch; ++k, ++enq) {

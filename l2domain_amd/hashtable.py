@@ -4,7 +4,8 @@ Mirrors the reference's hash application (applications/hash/src/hash_probe_dep.c
 "baseline"/"oblivious" is probe_dep_base (:66-83), "aware" the side-routed probe_dep_sa
 (:85-116) -- here the keys are routed to the I/O die that homes their slot -- and
 "swapped"/"rotated" its swapped launch (:317-323). The reference builds the table on the
-CPU (:226-241); this table is filled on the GPU by `insert`.
+CPU (:226-241); this table is filled on the GPU, by `build` (the whole table from scratch, range
+by range in LDS) or by `insert` (compare-and-swap claims into a table that may hold keys).
 """
 from __future__ import annotations
 

@@ -50,6 +50,13 @@ constexpr int kMergeBins = 1024;  // bins per merge unit (4 per thread)
 constexpr int kMergeUnitsPerBucket = kBucketBins / kMergeBins;
 constexpr uint32_t kSpareKey = (uint32_t)kMaxBuckets << kHB;  // above every valid key (num_bins <= 2^24)
 constexpr uint32_t kColCounters = 2048;  // partition counters per tile (buckets x columns)
+// Heavy hitter peeled in the partition: each tile's row of `offs` holds the nb + 1 bucket
+// offsets, then {key, count} of the tile's peeled key (kNoKey: none). One key: a second
+// compare per key took the kernel to 106 scalar registers and one workgroup per CU.
+constexpr int kPeelWords = 2;
+constexpr int kPeelCand = 8;       // candidates voted per tile: the first key of lanes 0..7 of wave 0
+constexpr uint32_t kPeelMin = 8;   // ... peeled when at least 8 of the 256 samples match
+constexpr uint32_t kNoKey = 0xffffffffu;
 
 struct HistBucket {
     int first;  // first item (= partial slot) of this bucket
@@ -84,7 +91,7 @@ static HistLayout hist_layout(size_t n, uint32_t num_bins) {
     L.partials = o;
     o = align256(o + (size_t)L.nitems * kBucketBins * sizeof(uint32_t));
     L.offs = o;
-    o = align256(o + (size_t)L.ntiles * (L.nb + 1) * sizeof(uint32_t));
+    o = align256(o + (size_t)L.ntiles * (L.nb + 1 + kPeelWords) * sizeof(uint32_t));
     L.part = o;
     o = align256(o + (size_t)L.ntiles * kTileKeys * sizeof(uint16_t));
     L.total = o;
@@ -143,6 +150,7 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
     __shared__ uint32_t col[kColCounters + kWave];
     __shared__ uint32_t wsum[kP1Threads / kWave];
     __shared__ uint32_t s_total;
+    __shared__ uint32_t s_hot, s_hotc;
     __shared__ __attribute__((aligned(16))) uint16_t stage[kTileKeys + 8];
     constexpr bool VEC = KIND != kPartRange;
     const int g = (int)blockIdx.x;
@@ -233,7 +241,43 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
                 kk[4 * j + c] = idx < src.r1 ? src.keys[idx] : 0xffffffffu;
             }
     }
+    // Heavy hitter: wave 0 votes the tile's most frequent key among kPeelCand candidates on
+    // 256 samples (the first four keys of each lane); every thread then counts that key in a
+    // register and makes it a spare, so it is neither staged nor written: under a skewed
+    // stream it is a large share of the u16 offsets the count pass would read back. The
+    // tile's {key, count} goes after its bucket offsets; the count pass adds it.
+    if (VEC && wave == 0) {
+        uint32_t b1 = kNoKey, c1 = 0;
+#pragma unroll 1
+        for (int j = 0; j < kPeelCand; ++j) {
+            const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)kk[0], j);
+            const uint32_t m = (kk[0] == c ? 1u : 0u) + (kk[1] == c ? 1u : 0u) + (kk[2] == c ? 1u : 0u) +
+                               (kk[3] == c ? 1u : 0u);
+            const uint32_t n = wave_sum_u32(m);
+            if (c != spare && n > c1) {  // wave-uniform
+                b1 = c;
+                c1 = n;
+            }
+        }
+        if (lane == 0) {
+            s_hot = c1 >= kPeelMin ? b1 : kNoKey;
+            s_hotc = 0;
+        }
+    }
     __syncthreads();
+    uint32_t h1 = kNoKey;
+    if (VEC) {
+        h1 = s_hot;
+        uint32_t n1 = 0;
+#pragma unroll
+        for (int j = 0; j < 4 * kP1Vec; ++j) {
+            const bool m1 = kk[j] == h1;
+            n1 += m1 ? 1u : 0u;
+            kk[j] = m1 ? spare : kk[j];
+        }
+        n1 = wave_sum_u32(n1);
+        if (lane == 0 && n1) atomicAdd(&s_hotc, n1);
+    }
 
     // Counter index of a key: its bucket's row, this lane's column (a spare key's row is past
     // the table, so the clamp sends it to this lane's spare counter). Packed (at most
@@ -295,7 +339,7 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
     if (tid < kWave) col[kColCounters + tid] = kTileKeys;  // spare slots land on stage[kTileKeys]
     __syncthreads();
 
-    uint32_t *my_offs = offs + (size_t)t * (nb + 1);
+    uint32_t *my_offs = offs + (size_t)t * (nb + 1 + kPeelWords);
     uint32_t *my_tot = tot + (size_t)(t % kNumXcd) * nb;
 #pragma unroll
     for (int j = 0; j < 4 * kP1Vec; ++j) {
@@ -315,7 +359,14 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
         my_offs[b] = start;
         if (end > start) atomicAdd(&my_tot[b], end - start);
     }
-    if (tid == 0) my_offs[nb] = tile_total;
+    if (tid == 0) {
+        my_offs[nb] = tile_total;
+        my_offs[nb + 1] = h1;  // s_hotc is final: every wave added before the last barriers
+        my_offs[nb + 2] = VEC ? s_hotc : 0u;
+        // a bucket whose keys were all peeled still needs a counting item, which the plan
+        // deals only to buckets with a non-zero total: one unit per peeling tile is enough
+        if (VEC && h1 != kNoKey && s_hotc) atomicAdd(&my_tot[h1 >> kHB], 1u);
+    }
 
     const uint32_t nvec = (tile_total + 7) / 8;  // 8 u16 per 16-byte store
     const uint4 *from = reinterpret_cast<const uint4 *>(stage);
@@ -439,6 +490,14 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     struct {
         int t0, t1;
     } const it{s_item[1], s_item[2]};
+    // The heavy hitters the partition peeled from this item's tiles, where they fall in this
+    // bucket: every tile's {key, count} is added by the one item of its key's bucket whose
+    // tile range holds the tile.
+    for (int tt = it.t0 + tid; tt < it.t1; tt += kP2Threads) {
+        const uint32_t *pw = offs + (size_t)tt * (nb + 1 + kPeelWords) + nb + 1;
+        const uint32_t k1 = pw[0], n1 = pw[1];
+        if (k1 != kNoKey && (int)(k1 >> kHB) == b && n1) atomicAdd(&h[k1 & (kBucketBins - 1)], n1);
+    }
     uint32_t hot = kTrash + 1, hot2 = kTrash + 2;  // no hot keys yet (never equal, never a key)
     uint32_t hc = 0, hc2 = 0;
     auto flush_hot2 = [&]() {
@@ -463,7 +522,7 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     for (int tb = it.t0 + wave; tb < it.t1; tb += kP2Waves * kWave) {
         const int tl = tb + lane * kP2Waves;
         const bool tok = tl < it.t1;
-        const uint32_t *o = offs + (size_t)(tok ? tl : it.t1 - 1) * (nb + 1) + b;
+        const uint32_t *o = offs + (size_t)(tok ? tl : it.t1 - 1) * (nb + 1 + kPeelWords) + b;
         const uint32_t rs0 = o[0], re0 = o[1];
         const uint32_t rs = tok ? rs0 : 0u, re = tok ? re0 : 0u;
         const uint32_t nvec = re > rs ? ((re + 7) >> 3) - (rs >> 3) : 0u;

@@ -48,7 +48,7 @@ MODES = ("oblivious", "aware", "rotated")
 # launches. Atomic and random-access kernels move whole requests (a 16-byte CAS or probe
 # costs a request each way).
 TRAFFIC = {
-    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1614009616,
+    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1565600521,
     ("hash_2p26_lf0.5_u64", "warm", "aware"): 20180216301,
     ("hist256_bytes_512MiB_mix32", "warm", "aware"): 545405734,
     ("hist256_bytes_512MiB_mix32", "cold", "aware"): 545042400,

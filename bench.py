@@ -48,19 +48,19 @@ MODES = ("oblivious", "aware", "rotated")
 # launches. Atomic and random-access kernels move whole requests (a 16-byte CAS or probe
 # costs a request each way).
 TRAFFIC = {
-    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1565600521,
-    ("hash_2p26_lf0.5_u64", "warm", "aware"): 20180216301,
-    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 545405734,
-    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 545042400,
-    ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245587489,
-    ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3925728225,
-    ("bfs_rmat22_ef16", "warm", "aware"): 239009619,
-    ("gemv_f32_4096x4096", "warm", "aware"): 67728407,
-    ("gemv_f32_4096x4096", "cold", "aware"): 67726960,
-    ("gemv_f16_14336x4096", "warm", "aware"): 117662518,
-    ("gemv_f16_14336x4096", "cold", "aware"): 117663801,
-    ("gemv_f16_4096x14336", "warm", "aware"): 118194240,
-    ("gemv_f16_4096x14336", "cold", "aware"): 118199809,
+    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1565490535,
+    ("hash_2p26_lf0.5_u64", "warm", "aware"): 20178651279,
+    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 545040582,
+    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 544789343,
+    ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 246255500,
+    ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3930886610,
+    ("bfs_rmat22_ef16", "warm", "aware"): 238954307,
+    ("gemv_f32_4096x4096", "warm", "aware"): 67722242,
+    ("gemv_f32_4096x4096", "cold", "aware"): 67720303,
+    ("gemv_f16_14336x4096", "warm", "aware"): 117650715,
+    ("gemv_f16_14336x4096", "cold", "aware"): 117652280,
+    ("gemv_f16_4096x14336", "warm", "aware"): 118182497,
+    ("gemv_f16_4096x14336", "cold", "aware"): 118188244,
 }
 
 

@@ -57,6 +57,23 @@ constexpr int kPeelWords = 2;
 constexpr int kPeelCand = 8;       // candidates voted per tile: the first key of lanes 0..7 of wave 0
 constexpr uint32_t kPeelMin = 8;   // ... peeled when at least 8 of the 256 samples match
 constexpr uint32_t kNoKey = 0xffffffffu;
+// Hot-key table: a sampling pass picks up to kHotSlots keys drawn at least kHotMin times
+// among kHotSamples sampled keys; the partition counts them in LDS (one dense row of
+// kHotSlots counters per tile) instead of writing their u16 offsets, and the count pass adds
+// those rows into its bucket's histogram. A key's slot is direct-mapped (hot_slot(key)); a
+// tile's row holds the slots' counters in key order (slot i at row position perm[i]), so the
+// hot keys of one bucket hold a contiguous range of every row.
+constexpr int kHotSlots = 256;
+constexpr int kHotCopies = 8;  // partition: lane l counts a hot key in copy l % 8 of its counter (4: +6 us)
+constexpr int kHotSamples = 8192;
+constexpr int kHotBlocks = 32;               // samples: 32 runs of 256 consecutive keys, evenly spaced
+constexpr int kHotTable = 16384;             // sampling pass: open-addressed LDS table (128 KB)
+constexpr uint32_t kHotMin = 2;
+constexpr size_t kHotMinKeys = size_t(1) << 20;  // smaller calls skip the sampling launch
+// hot region of the workspace: tab[kHotSlots] (key or kNoKey), perm[kHotSlots] (row position
+// of each slot), sorted[kHotSlots] (key at each row position), first[kMaxBuckets + 1]
+constexpr int kHotTab = 0, kHotPerm = kHotSlots, kHotSorted = 2 * kHotSlots, kHotFirst = 3 * kHotSlots;
+constexpr int kHotWords = 3 * kHotSlots + kMaxBuckets + 1;
 
 struct HistBucket {
     int first;  // first item (= partial slot) of this bucket
@@ -65,7 +82,7 @@ struct HistBucket {
 
 struct HistLayout {
     int nb, ntiles, per_xcd, nitems;
-    size_t part, offs, tot, buckets, partials, total;
+    size_t part, offs, tot, buckets, partials, hot, hot_part, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -94,6 +111,11 @@ static HistLayout hist_layout(size_t n, uint32_t num_bins) {
     o = align256(o + (size_t)L.ntiles * (L.nb + 1 + kPeelWords) * sizeof(uint32_t));
     L.part = o;
     o = align256(o + (size_t)L.ntiles * kTileKeys * sizeof(uint16_t));
+    // hot-key table (kHotWords), then one row of kHotSlots counters per tile
+    L.hot = o;
+    o = align256(o + (size_t)kHotWords * sizeof(uint32_t));
+    L.hot_part = o;
+    o = align256(o + (size_t)L.ntiles * kHotSlots * sizeof(uint32_t));
     L.total = o;
     return L;
 }
@@ -105,6 +127,113 @@ __device__ __forceinline__ uint4 load_stream(const uint4 *p) {
     typedef unsigned int v4u __attribute__((ext_vector_type(4)));
     const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(p));
     return make_uint4(t.x, t.y, t.z, t.w);
+}
+
+// ---------------------------------------------------------------------------------------
+// 0. hot keys (one workgroup): which keys the partition counts in LDS
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t hot_slot(uint32_t key) { return (key * 0x9E3779B1u) >> 24; }
+
+// Samples kHotSamples keys (kHotBlocks evenly spaced runs of consecutive keys: one page
+// each, where single keys spread over the whole array cost a translation miss apiece), counts
+// them in an open-addressed LDS table, and gives each direct-mapped slot the most sampled key
+// that maps to it (at least kHotMin samples; ties to the larger key, so the table is a
+// function of the keys alone). Which keys are hot changes where they are counted, never the
+// counts. Needs n >= kHotSamples.
+__global__ void __launch_bounds__(1024) hist_hot_kernel(const uint32_t *__restrict__ keys, size_t n, uint32_t num_bins,
+                                                        int nb, uint32_t *__restrict__ hot) {
+    constexpr int kPer = kHotSamples / 1024;
+    constexpr int kRun = kHotSamples / kHotBlocks;
+    __shared__ uint32_t tk[kHotTable], tc[kHotTable];
+    __shared__ unsigned long long best[kHotSlots];
+    __shared__ __attribute__((aligned(16))) uint32_t skey[kHotSlots];
+    __shared__ uint32_t ssorted[kHotSlots], s_rank[kHotSlots];
+    __shared__ uint32_t s_empty[kHotSlots / kWave], s_valid;
+    const int tid = (int)threadIdx.x;
+    uint32_t smp[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int i = tid + k * 1024;
+        smp[k] = keys[(size_t)(i / kRun) * (n / kHotBlocks) + (size_t)(i % kRun)];
+    }
+    for (int i = tid; i < kHotTable; i += 1024) {
+        tk[i] = kNoKey;
+        tc[i] = 0;
+    }
+    if (tid < kHotSlots) best[tid] = 0ull;
+    __syncthreads();
+#pragma unroll 1
+    for (int k = 0; k < kPer; ++k) {
+        const uint32_t key = smp[k];
+        if (key >= num_bins) continue;
+        uint32_t h = (key * 0x85EBCA6Bu) >> (32 - 14);
+        // kHotSamples < kHotTable: a free or matching entry is always found
+        for (int probe = 0; probe < kHotTable; ++probe) {
+            // a plain read first: a sampled key is mostly already there, and a compare-and-swap
+            // of many lanes on one hot key's entry serialises
+            uint32_t cur = tk[h];
+            if (cur == kNoKey) cur = atomicCAS(&tk[h], kNoKey, key);
+            if (cur == kNoKey || cur == key) {
+                atomicAdd(&tc[h], 1u);
+                break;
+            }
+            h = (h + 1) & (kHotTable - 1);
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < kHotTable; i += 1024) {
+        const uint32_t key = tk[i], c = tc[i];
+        if (key != kNoKey && c >= kHotMin) atomicMax(&best[hot_slot(key)], ((unsigned long long)c << 32) | key);
+    }
+    __syncthreads();
+    if (tid < kHotSlots) skey[tid] = best[tid] ? (uint32_t)best[tid] : kNoKey;
+    __syncthreads();
+    // row position of slot i: the rank of its key among the valid keys (distinct; kNoKey sorts
+    // last), empty slots after them in slot order (their place from the waves' ballots)
+    if (tid < kHotSlots) {
+        const uint32_t key = skey[tid];
+        const int lane = tid % kWave, wave = tid / kWave;
+        const uint64_t empty = __ballot(key == kNoKey);
+        if (lane == 0) s_empty[wave] = (uint32_t)__builtin_popcountll(empty);
+        uint32_t below = 0;
+        const uint4 *s4 = reinterpret_cast<const uint4 *>(skey);
+#pragma unroll 16
+        for (int q = 0; q < kHotSlots / 4; ++q) {
+            const uint4 v = s4[q];
+            below += (v.x < key ? 1u : 0u) + (v.y < key ? 1u : 0u) + (v.z < key ? 1u : 0u) + (v.w < key ? 1u : 0u);
+        }
+        s_rank[tid] = below;
+    }
+    __syncthreads();
+    if (tid < kHotSlots) {
+        const uint32_t key = skey[tid];
+        const int lane = tid % kWave, wave = tid / kWave;
+        uint32_t nempty = 0, empty_before = 0;
+        for (int w = 0; w < kHotSlots / kWave; ++w) {
+            nempty += s_empty[w];
+            empty_before += w < wave ? s_empty[w] : 0u;
+        }
+        const uint64_t empty = __ballot(key == kNoKey);
+        empty_before += (uint32_t)__builtin_popcountll(empty & ((1ull << lane) - 1));
+        const uint32_t nvalid = kHotSlots - nempty;
+        const uint32_t pos = key != kNoKey ? s_rank[tid] : nvalid + empty_before;
+        hot[kHotTab + tid] = key;
+        hot[kHotPerm + tid] = pos;
+        hot[kHotSorted + pos] = key;
+        ssorted[pos] = key;
+        if (tid == 0) s_valid = nvalid;
+    }
+    __syncthreads();
+    // first[b]: the row position of bucket b's first key (a binary search over the sorted keys)
+    for (int b = tid; b <= nb; b += 1024) {
+        uint32_t lo = 0, hi = s_valid;
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) / 2;
+            if ((ssorted[mid] >> kHB) < (uint32_t)b) lo = mid + 1;
+            else hi = mid;
+        }
+        hot[kHotFirst + b] = lo;
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -139,9 +268,9 @@ static_assert(kP1Threads / kWave * 4 * kP1Vec * (kWave * kPackBuckets / kColCoun
               "packed slots overflow");
 
 template <int KIND, bool PACK>
-__global__ void __launch_bounds__(kP1Threads)
-hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restrict__ part,
-                      uint32_t *__restrict__ offs, uint32_t *__restrict__ tot) {
+__device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restrict__ part,
+                                               uint32_t *__restrict__ offs, uint32_t *__restrict__ tot,
+                                               const uint32_t *__restrict__ hot, uint32_t *__restrict__ hot_part) {
     // Every bucket's counter is split into S columns, column = lane % S (S = 64 for up to
     // 32 buckets), laid out col[b * S + s]: the lanes of one LDS add never share an address,
     // so a wave's 64 adds do not serialise on a popular bucket. col[kColCounters + s] and
@@ -151,6 +280,7 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
     __shared__ uint32_t wsum[kP1Threads / kWave];
     __shared__ uint32_t s_total;
     __shared__ uint32_t s_hot, s_hotc;
+    __shared__ uint32_t s_tab[kHotSlots], s_cnt[kHotSlots * kHotCopies];
     __shared__ __attribute__((aligned(16))) uint16_t stage[kTileKeys + 8];
     constexpr bool VEC = KIND != kPartRange;
     const int g = (int)blockIdx.x;
@@ -241,6 +371,18 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
                 kk[4 * j + c] = idx < src.r1 ? src.keys[idx] : 0xffffffffu;
             }
     }
+    // The hot-key table, loaded after the keys (its LDS store then waits for them too,
+    // which the vote below does anyway; loaded first, it put a round trip before them).
+    // (kinds that run in calls with a table: packed, and the range kind beside them, whose
+    // tiles write zero rows)
+    constexpr bool HOT = PACK || KIND == kPartRange;
+    uint32_t my_perm = 0;
+    if (HOT && hot != nullptr && tid < kHotSlots) {
+        s_tab[tid] = hot[kHotTab + tid];
+        my_perm = hot[kHotPerm + tid];
+#pragma unroll
+        for (int c = 0; c < kHotCopies; ++c) s_cnt[tid * kHotCopies + c] = 0;
+    }
     // Heavy hitter: wave 0 votes the tile's most frequent key among kPeelCand candidates on
     // 256 samples (the first four keys of each lane); every thread then counts that key in a
     // register and makes it a spare, so it is neither staged nor written: under a skewed
@@ -277,6 +419,26 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
         }
         n1 = wave_sum_u32(n1);
         if (lane == 0 && n1) atomicAdd(&s_hotc, n1);
+        // keys of the hot table: counted in LDS and made spares (hot is null for calls that
+        // have no table; the unpacked kinds, at 64 registers already, never look up)
+        // (the table's keys are below num_bins, so a spare never matches; every read of a
+        // batch is issued before its adds, which the compiler cannot reorder past them)
+        if (PACK && hot != nullptr) {
+            constexpr int kBatch = 2 * kP1Vec;
+#pragma unroll
+            for (int j0 = 0; j0 < 4 * kP1Vec; j0 += kBatch) {
+                uint32_t e[kBatch];
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j) e[j] = s_tab[hot_slot(kk[j0 + j])];
+#pragma unroll
+                for (int j = 0; j < kBatch; ++j) {
+                    if (e[j] == kk[j0 + j]) {
+                        atomicAdd(&s_cnt[hot_slot(kk[j0 + j]) * kHotCopies + (lane & (kHotCopies - 1))], 1u);
+                        kk[j0 + j] = spare;
+                    }
+                }
+            }
+        }
     }
 
     // Counter index of a key: its bucket's row, this lane's column (a spare key's row is past
@@ -367,11 +529,39 @@ hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restri
         // deals only to buckets with a non-zero total: one unit per peeling tile is enough
         if (VEC && h1 != kNoKey && s_hotc) atomicAdd(&my_tot[h1 >> kHB], 1u);
     }
+    if (HOT && hot != nullptr && tid < kHotSlots) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int k = 0; k < kHotCopies; ++k) c += s_cnt[tid * kHotCopies + k];
+        hot_part[(size_t)t * kHotSlots + my_perm] = c;
+    }
 
     const uint32_t nvec = (tile_total + 7) / 8;  // 8 u16 per 16-byte store
     const uint4 *from = reinterpret_cast<const uint4 *>(stage);
     uint4 *dst = reinterpret_cast<uint4 *>(part + (size_t)t * kTileKeys);
     for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) dst[i] = from[i];
+}
+
+// Two workgroups of 16 waves share a CU only while a wave holds at most 80 scalar registers
+// in all (measured: the routed packed kind at 82 ran at half the resident waves, 408 against
+// 286 us at 2^28 keys, though the compiler's occupancy estimate said 8 waves per SIMD), so
+// the packed kinds, which carry the hot-key lookups, are capped; the unpacked ones stay
+// within 80 uncapped, and the cap would cost them a vector register past 64.
+constexpr int kPartPackedSgprs = 74;
+
+template <int KIND>
+__global__ void __launch_bounds__(kP1Threads) __attribute__((amdgpu_num_sgpr(kPartPackedSgprs)))
+hist_partition_packed_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restrict__ part,
+                             uint32_t *__restrict__ offs, uint32_t *__restrict__ tot, const uint32_t *__restrict__ hot,
+                             uint32_t *__restrict__ hot_part) {
+    partition_tile<KIND, true>(src, num_bins, nb, part, offs, tot, hot, hot_part);
+}
+
+template <int KIND>
+__global__ void __launch_bounds__(kP1Threads)
+hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restrict__ part, uint32_t *__restrict__ offs,
+                      uint32_t *__restrict__ tot, const uint32_t *__restrict__ hot, uint32_t *__restrict__ hot_part) {
+    partition_tile<KIND, false>(src, num_bins, nb, part, offs, tot, hot, hot_part);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -406,12 +596,16 @@ struct Deal {
 // slot nzpre + floor(pre * R / N), R = slots beyond one per non-empty bucket, and the slots
 // end exactly at nitems (the clamps only guard the table).
 template <int THREADS>
-__device__ Deal deal_items(const uint32_t *__restrict__ tot, int nb, int nitems, uint32_t *wsum) {
+__device__ Deal deal_items(const uint32_t *__restrict__ tot, int nb, int nitems, uint32_t *wsum,
+                           const uint32_t *__restrict__ hot_first) {
     __shared__ uint32_t s_total, s_nnz;
     const int b = (int)threadIdx.x;
     uint32_t T = 0;
-    if (b < nb)
+    if (b < nb) {
         for (int x = 0; x < kNumXcd; ++x) T += tot[(size_t)x * nb + b];
+        // a bucket with hot-table keys needs a counting item even if all its keys were hot
+        if (hot_first != nullptr && hot_first[b + 1] > hot_first[b]) T += 1;
+    }
     const uint32_t nz = (b < nb && T > 0) ? 1u : 0u;
     const uint32_t pre = block_excl_scan<THREADS>(T, wsum, &s_total);
     const uint32_t N = s_total;
@@ -459,7 +653,8 @@ __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t 
 __global__ void __launch_bounds__(kP2Threads)
 hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb, int ntiles,
                   const uint32_t *__restrict__ tot, int per_xcd, uint32_t *__restrict__ partials,
-                  HistBucket *__restrict__ buckets, int mode, unsigned rot) {
+                  HistBucket *__restrict__ buckets, int mode, unsigned rot, const uint32_t *__restrict__ hot_tab,
+                  const uint32_t *__restrict__ hot_part) {
     __shared__ __attribute__((aligned(16))) uint32_t h[kCountSlots];
     __shared__ uint32_t wsum[kP2Waves];
     __shared__ int s_item[3];  // bucket (-1: idle slot), t0, t1
@@ -474,7 +669,8 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     }
     if (tid == 0) s_item[0] = -1;
     const int nitems = per_xcd * kNumXcd;
-    const Deal d = deal_items<kP2Threads>(tot, nb, nitems, wsum);  // synchronises the block
+    const uint32_t *hot_first = hot_tab != nullptr ? hot_tab + kHotFirst : nullptr;
+    const Deal d = deal_items<kP2Threads>(tot, nb, nitems, wsum, hot_first);  // synchronises the block
     if (tid < nb && d.count > 0 && (uint32_t)slot >= d.first && (uint32_t)slot < d.first + d.count) {
         const uint32_t j = (uint32_t)slot - d.first;
         s_item[0] = tid;
@@ -497,6 +693,28 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
         const uint32_t *pw = offs + (size_t)tt * (nb + 1 + kPeelWords) + nb + 1;
         const uint32_t k1 = pw[0], n1 = pw[1];
         if (k1 != kNoKey && (int)(k1 >> kHB) == b && n1) atomicAdd(&h[k1 & (kBucketBins - 1)], n1);
+    }
+    // The hot-table keys of this bucket (ranks [lo, lo + m)): a group of P threads per key sums
+    // its counters over the item's tiles, eight loads in flight per thread.
+    if (hot_tab != nullptr) {
+        const int lo = (int)hot_first[b], m = (int)hot_first[b + 1] - lo;
+        if (m > 0) {
+            const int P = kP2Threads / m;  // m <= kHotSlots: at least 4 threads per key
+            const int j = tid / P, r = tid % P;
+            if (j < m) {
+                const uint32_t *col = hot_part + lo + j;
+                uint32_t acc = 0;
+                constexpr int U = 8;
+                for (int tt = it.t0 + r; tt < it.t1; tt += U * P) {
+                    uint32_t v[U];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) v[u] = col[(size_t)min(tt + u * P, it.t1 - 1) * kHotSlots];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) acc += tt + u * P < it.t1 ? v[u] : 0u;
+                }
+                if (acc) atomicAdd(&h[hot_tab[kHotSorted + lo + j] & (kBucketBins - 1)], acc);
+            }
+        }
     }
     uint32_t hot = kTrash + 1, hot2 = kTrash + 2;  // no hot keys yet (never equal, never a key)
     uint32_t hc = 0, hc2 = 0;
@@ -745,22 +963,31 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
 
     // From the first launch on, an error return leaves the workspace's bucket totals
     // non-zero: the caller must zero-fill the workspace again before its next use.
-    using PartKernel = void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *);
+    // Hot-key table: for calls of at least kHotMinKeys keys into at most kPackBuckets buckets
+    // (the packed partition: the unpacked one has no registers left for the lookups).
+    uint32_t *hot = nullptr;
+    uint32_t *hot_part = reinterpret_cast<uint32_t *>(ws + L.hot_part);
+    if (n >= kHotMinKeys && pack) {
+        hot = reinterpret_cast<uint32_t *>(ws + L.hot);
+        launch("hist_hot_kernel", hist_hot_kernel, dim3(1), dim3(1024), 0, s, keys, n, num_bins, L.nb, hot);
+        if (int rc = launch_status("hist_hot_kernel")) return rc;
+    }
+    using PartKernel = void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *, const uint32_t *, uint32_t *);
     for (int k = 0; k < nplan; ++k) {
         const PartLaunch &pl = plan[k];
         PartKernel kern;
         if (pl.kind == kPartRouted)
-            kern = pack ? hist_partition_kernel<kPartRouted, true> : hist_partition_kernel<kPartRouted, false>;
+            kern = pack ? hist_partition_packed_kernel<kPartRouted> : hist_partition_kernel<kPartRouted>;
         else if (pl.kind == kPartFull)
-            kern = pack ? hist_partition_kernel<kPartFull, true> : hist_partition_kernel<kPartFull, false>;
+            kern = pack ? hist_partition_packed_kernel<kPartFull> : hist_partition_kernel<kPartFull>;
         else
-            kern = hist_partition_kernel<kPartRange, false>;
+            kern = hist_partition_kernel<kPartRange>;
         launch("hist_partition_kernel", kern, dim3(pl.grid), dim3(kP1Threads), 0, s, pl.ps, num_bins, L.nb, part, offs,
-               tot);
+               tot, hot, hot_part);
         if (int rc = launch_status("hist_partition_kernel")) return rc;
     }
     launch("hist_count_kernel", hist_count_kernel, dim3(L.nitems), dim3(kP2Threads), 0, s, part, offs, L.nb, ntl, tot,
-           L.per_xcd, partials, buckets, mode, rot_eff);
+           L.per_xcd, partials, buckets, mode, rot_eff, hot, hot_part);
     if (int rc = launch_status("hist_count_kernel")) return rc;
     // one workgroup per merge unit, up to 4096
     const int merge_grid = std::min(std::max(L.nb * kMergeUnitsPerBucket, kNumXcd * 64), 4096);

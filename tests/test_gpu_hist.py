@@ -58,7 +58,8 @@ def test_unaligned_keys(n, mode):
 
 
 @pytest.mark.parametrize("mode", MODES)
-@pytest.mark.parametrize("skip,n", [(1028, 5 * 65536 + 12345), (0, 3 * 65536), (4, 65536 + 4096 * 7 + 3)])
+@pytest.mark.parametrize("skip,n", [(1028, 5 * 65536 + 12345), (0, 3 * 65536), (4, 65536 + 4096 * 7 + 3),
+                                    (1028, (1 << 21) + 12345)])
 def test_routed_tiles_with_home_map(skip, n, mode):
     """Aware and rotated calls read whole groups of 16 KiB pairs by home die; keys before the
     first pair (`skip` words into a 2 MiB-aligned buffer) and after the last group go through
@@ -120,6 +121,27 @@ def test_hot_table_cases(case, mode):
     ref, _ = ora.histogram(keys, num_bins, nthreads=16)
     print(case, mode, len(keys), num_bins, flush=True)
     np.testing.assert_array_equal(gpu_hist(keys, num_bins, mode), ref)
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("offset,n,num_bins", [(0, 1 << 20, 1 << 16), (0, (1 << 20) - 1, 1 << 20),
+                                               (1, (1 << 20) + 5, 1 << 20), (3, (1 << 21) + 3, 1 << 20),
+                                               (0, (1 << 21) + 7, (1 << 20) + 1)])
+def test_hot_table_sizes_and_alignment(offset, n, num_bins, mode):
+    """Zipf keys around the sampling pass's threshold (2^20 keys: the hot-key table is built
+    and used from there up, for at most 2^20 bins): keys that start 4 or 12 bytes past a
+    16-byte boundary (every tile on the per-key path, whose tiles add nothing to the table's
+    counters), and a bin count one past the packed partition (no table)."""
+    k = gen.zipf_keys_device(n + offset, min(num_bins, 1 << 20), 4000 + n, ZIPF_S)
+    view = k[offset:]
+    assert (view.data_ptr() % 16) == 4 * offset % 16
+    keys = view.cpu().numpy().view(np.uint32)
+    ref, _ = ora.histogram(keys, num_bins, nthreads=16)
+    counts = torch.full((num_bins,), -7, dtype=torch.int32, device="cuda")
+    Histogram(n, num_bins)(view, counts, mode=mode)
+    torch.cuda.synchronize()
+    print(offset, n, num_bins, mode, flush=True)
+    np.testing.assert_array_equal(counts.cpu().numpy().view(np.uint32), ref)
 
 
 @pytest.fixture(scope="module")

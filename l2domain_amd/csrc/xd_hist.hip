@@ -132,7 +132,10 @@ __device__ __forceinline__ uint4 load_stream(const uint4 *p) {
 // ---------------------------------------------------------------------------------------
 // 0. hot keys (one workgroup): which keys the partition counts in LDS
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t hot_slot(uint32_t key) { return (key * 0x9E3779B1u) >> 24; }
+// A key's slot: its low bits (one VALU op: the partition is bound by VALU issue, where a
+// multiplicative hash's 32-bit multiply ran at a quarter of the rate). Consecutive hot keys
+// get distinct slots; keys equal in their low 8 bits share one, the most sampled winning it.
+__device__ __forceinline__ uint32_t hot_slot(uint32_t key) { return key & (kHotSlots - 1); }
 
 // Samples kHotSamples keys (kHotBlocks evenly spaced runs of consecutive keys: one page
 // each, where single keys spread over the whole array cost a translation miss apiece), counts
@@ -283,7 +286,9 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
     __shared__ uint32_t wsum[kP1Threads / kWave];
     __shared__ uint32_t s_total;
     __shared__ uint32_t s_hot, s_hotc;
-    __shared__ uint32_t s_tab[kHotSlots], s_cnt[kHotSlots * kHotCopies];
+    // hot counters: copy c of slot i at s_cnt[c * (kHotSlots + 1) + i] (rows padded so that the
+    // copies of one slot sit in different banks)
+    __shared__ uint32_t s_tab[kHotSlots], s_cnt[(kHotSlots + 1) * kHotCopies];
     __shared__ __attribute__((aligned(16))) uint16_t stage[kTileKeys + 8];
     constexpr bool VEC = KIND != kPartRange;
     const int g = (int)blockIdx.x;
@@ -384,7 +389,7 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
         s_tab[tid] = hot[kHotTab + tid];
         my_perm = hot[kHotPerm + tid];
 #pragma unroll
-        for (int c = 0; c < kHotCopies; ++c) s_cnt[tid * kHotCopies + c] = 0;
+        for (int c = 0; c < kHotCopies; ++c) s_cnt[c * (kHotSlots + 1) + tid] = 0;
     }
     // Heavy hitter: wave 0 votes the tile's most frequent key among kPeelCand candidates on
     // 256 samples (the first four keys of each lane); every thread then counts that key in a
@@ -393,8 +398,9 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
     // tile's {key, count} goes after its bucket offsets; the count pass adds it.
     if (VEC && wave == 0) {
         uint32_t b1 = kNoKey, c1 = 0;
+        // (no vote with a hot-key table, which holds the tile's top key too)
 #pragma unroll 1
-        for (int j = 0; j < kPeelCand; ++j) {
+        for (int j = 0; j < (hot == nullptr ? kPeelCand : 0); ++j) {
             const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)kk[0], j);
             const uint32_t m = (kk[0] == c ? 1u : 0u) + (kk[1] == c ? 1u : 0u) + (kk[2] == c ? 1u : 0u) +
                                (kk[3] == c ? 1u : 0u);
@@ -413,21 +419,24 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
     uint32_t h1 = kNoKey;
     if (VEC) {
         h1 = s_hot;
-        uint32_t n1 = 0;
+        if (h1 != kNoKey) {  // (uniform)
+            uint32_t n1 = 0;
 #pragma unroll
-        for (int j = 0; j < 4 * kP1Vec; ++j) {
-            const bool m1 = kk[j] == h1;
-            n1 += m1 ? 1u : 0u;
-            kk[j] = m1 ? spare : kk[j];
+            for (int j = 0; j < 4 * kP1Vec; ++j) {
+                const bool m1 = kk[j] == h1;
+                n1 += m1 ? 1u : 0u;
+                kk[j] = m1 ? spare : kk[j];
+            }
+            n1 = wave_sum_u32(n1);
+            if (lane == 0 && n1) atomicAdd(&s_hotc, n1);
         }
-        n1 = wave_sum_u32(n1);
-        if (lane == 0 && n1) atomicAdd(&s_hotc, n1);
         // keys of the hot table: counted in LDS and made spares (hot is null for calls that
         // have no table; the unpacked kinds, at 64 registers already, never look up)
         // (the table's keys are below num_bins, so a spare never matches; every read of a
         // batch is issued before its adds, which the compiler cannot reorder past them)
         if (PACK && hot != nullptr) {
             constexpr int kBatch = 2 * kP1Vec;
+            uint32_t *my_cnt = s_cnt + (lane & (kHotCopies - 1)) * (kHotSlots + 1);
 #pragma unroll
             for (int j0 = 0; j0 < 4 * kP1Vec; j0 += kBatch) {
                 uint32_t e[kBatch];
@@ -436,7 +445,7 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
 #pragma unroll
                 for (int j = 0; j < kBatch; ++j) {
                     if (e[j] == kk[j0 + j]) {
-                        atomicAdd(&s_cnt[hot_slot(kk[j0 + j]) * kHotCopies + (lane & (kHotCopies - 1))], 1u);
+                        atomicAdd(&my_cnt[hot_slot(kk[j0 + j])], 1u);
                         kk[j0 + j] = spare;
                     }
                 }
@@ -535,7 +544,7 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
     if (HOT && hot != nullptr && tid < kHotSlots) {
         uint32_t c = 0;
 #pragma unroll
-        for (int k = 0; k < kHotCopies; ++k) c += s_cnt[tid * kHotCopies + k];
+        for (int k = 0; k < kHotCopies; ++k) c += s_cnt[k * (kHotSlots + 1) + tid];
         hot_part[(size_t)t * kHotSlots + my_perm] = c;
     }
 

@@ -557,9 +557,10 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
 // Two workgroups of 16 waves share a CU only while a wave holds at most 80 scalar registers
 // in all (measured: the routed packed kind at 82 ran at half the resident waves, 408 against
 // 286 us at 2^28 keys, though the compiler's occupancy estimate said 8 waves per SIMD), so
-// the packed kinds, which carry the hot-key lookups, are capped; the unpacked ones stay
-// within 80 uncapped, and the cap would cost them a vector register past 64.
-constexpr int kPartPackedSgprs = 74;
+// the packed kinds, which carry the hot-key lookups, are capped (78 requested gives 76 in
+// all; 74 gave 72 but spilled half again as many scalars to vector lanes); the unpacked ones
+// stay within 80 uncapped, and a cap would cost them a vector register past 64.
+constexpr int kPartPackedSgprs = 78;
 
 template <int KIND>
 __global__ void __launch_bounds__(kP1Threads) __attribute__((amdgpu_num_sgpr(kPartPackedSgprs)))

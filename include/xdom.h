@@ -273,14 +273,18 @@ int xd_gemv_f16f32(const uint16_t *W, const uint16_t *x, float *y, int M, int K,
 /* ------------------------------------------------------------------------------------ */
 
 /* Workspace bytes xd_hist_u32 needs for n keys and num_bins counters (0 if num_bins is out
- * of range). About 2 bytes per key plus 128 KB per counting workgroup. The workspace must be
+ * of range). About 2 bytes per key, 1 KiB per 24576-key tile (hot-key counters) and 128 KB
+ * per counting workgroup. The workspace must be
  * zero-filled once when allocated; every call leaves its counters zeroed again, and a
  * workspace sized for n keys serves any smaller n. Calls sharing one workspace must not
  * overlap. */
 size_t xd_hist_workspace_size(size_t n, uint32_t num_bins);
 
 /* Histogram of uint32 keys into num_bins (1..2^24) uint32 counters; keys >= num_bins are
- * not counted. Every counts[k] is written (no accumulation into counts). n < 2^32.
+ * not counted. Every counts[k] is written (no accumulation into counts). n < 2^32. Calls of
+ * at least 2^20 keys into at most 2^20 bins first sample the keys for up to 256 frequent
+ * ones, which are counted in LDS during the partition (one more launch; the counts do not
+ * depend on which keys it picks).
  * Replaces histogram256_chunked_kernel / histogram256_persistent_kernel /
  * merge_histogram256_kernel (applications/histogram/src/histogram256_sideaware.cu:51-157),
  * generalised from 256 byte-bins (add_word, :20-25) to one bin per key. XD_MODE_AWARE

@@ -702,7 +702,8 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     // The heavy hitters the partition peeled from this item's tiles, where they fall in this
     // bucket: every tile's {key, count} is added by the one item of its key's bucket whose
     // tile range holds the tile.
-    for (int tt = it.t0 + tid; tt < it.t1; tt += kP2Threads) {
+    // (calls with a hot-key table peel nothing)
+    for (int tt = it.t0 + tid; hot_tab == nullptr && tt < it.t1; tt += kP2Threads) {
         const uint32_t *pw = offs + (size_t)tt * (nb + 1 + kPeelWords) + nb + 1;
         const uint32_t k1 = pw[0], n1 = pw[1];
         if (k1 != kNoKey && (int)(k1 >> kHB) == b && n1) atomicAdd(&h[k1 & (kBucketBins - 1)], n1);

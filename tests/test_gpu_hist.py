@@ -92,9 +92,9 @@ def test_workspace_reuse_shrinking_input():
 
 def _hot_case_keys(case: str) -> tuple[np.ndarray, int]:
     """2^25 keys (over a thousand partition tiles) of skewed distributions: hot bins crowding
-    one bucket, one bucket only, one bin per key value, a single key. They load the partition's
-    counter columns unevenly, and the count pass's per-wave votes on its two peeled hot keys
-    keep switching or never switch."""
+    one bucket, one bucket only, one bin per key value, a single key, popular keys that all
+    share one slot of the sampled hot-key table (slot = low 8 bits). They load the partition's
+    counter columns and hot counters unevenly."""
     n = 1 << 25
     rng = np.random.default_rng(sum(map(ord, case)))
     # (the device generator matches the oracle's key by key: test_device_zipf_keys_match_oracle_generator)
@@ -111,11 +111,14 @@ def _hot_case_keys(case: str) -> tuple[np.ndarray, int]:
         return rng.integers(0, 1100, size=n).astype(np.uint32), 1000
     if case == "one_key":
         return np.full(n, 123457, dtype=np.uint32), 1 << 20
+    if case == "same_low_byte":   # 4096 popular keys, all multiples of 256: one hot-table slot
+        return (rng.zipf(1.3, size=n) % 4096 * 256).astype(np.uint32), 1 << 20
     raise ValueError(case)
 
 
 @pytest.mark.parametrize("mode", MODES)
-@pytest.mark.parametrize("case", ["zipf_identity", "zipf_scrambled", "one_bucket", "few_bins", "one_key"])
+@pytest.mark.parametrize("case", ["zipf_identity", "zipf_scrambled", "one_bucket", "few_bins", "one_key",
+                                  "same_low_byte"])
 def test_hot_table_cases(case, mode):
     keys, num_bins = _hot_case_keys(case)
     ref, _ = ora.histogram(keys, num_bins, nthreads=16)

@@ -646,6 +646,8 @@ constexpr uint32_t kCountSlots = kLaneTrash + kWave;
 // a wave hit one LDS address). Every key takes one ds_add, with no branch: keys outside the
 // run and hot keys are added to the lane's private trash slot `trash`, so the adds of one
 // instruction never meet on a dropped key's address.
+// (VOTE false: no register keys, for calls whose hot-key table took the popular keys out)
+template <bool VOTE>
 __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t e, uint32_t s0, uint32_t e0,
                                           uint32_t hot, uint32_t hot2, uint32_t &hc, uint32_t &hc2,
                                           uint32_t trash) {
@@ -656,10 +658,14 @@ __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t 
     for (int k = 0; k < 8; ++k) {
         uint32_t key = (k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu);
         key = (e + (uint32_t)k - s0 < len) ? key : trash;
-        const bool h1 = key == hot, h2 = key == hot2;  // a trash slot is never a hot key
-        hc += h1 ? 1u : 0u;
-        hc2 += h2 ? 1u : 0u;
-        atomicAdd(&h[(h1 | h2) ? trash : key], 1u);
+        if (VOTE) {
+            const bool h1 = key == hot, h2 = key == hot2;  // a trash slot is never a hot key
+            hc += h1 ? 1u : 0u;
+            hc2 += h2 ? 1u : 0u;
+            atomicAdd(&h[(h1 | h2) ? trash : key], 1u);
+        } else {
+            atomicAdd(&h[key], 1u);
+        }
     }
 }
 
@@ -832,8 +838,13 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
                 }
             }
             }
-            count_vec(h, qa, ea, sa, xa, hot, hot2, hc, hc2, kLaneTrash + (uint32_t)lane);
-            count_vec(h, qb, eb, sb, xb, hot, hot2, hc, hc2, kLaneTrash + (uint32_t)lane);
+            if (hot_tab == nullptr) {
+                count_vec<true>(h, qa, ea, sa, xa, hot, hot2, hc, hc2, kLaneTrash + (uint32_t)lane);
+                count_vec<true>(h, qb, eb, sb, xb, hot, hot2, hc, hc2, kLaneTrash + (uint32_t)lane);
+            } else {
+                count_vec<false>(h, qa, ea, sa, xa, hot, hot2, hc, hc2, kLaneTrash + (uint32_t)lane);
+                count_vec<false>(h, qb, eb, sb, xb, hot, hot2, hc, hc2, kLaneTrash + (uint32_t)lane);
+            }
             qa = na;
             qb = nb2;
             ea = fa;

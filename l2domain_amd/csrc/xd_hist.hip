@@ -147,6 +147,7 @@ __global__ void __launch_bounds__(1024) hist_hot_kernel(const uint32_t *__restri
                                                         int nb, uint32_t *__restrict__ hot) {
     constexpr int kPer = kHotSamples / 1024;
     constexpr int kRun = kHotSamples / kHotBlocks;
+    static_assert(1024 == 4 * kHotSlots, "the rank loop runs four threads per slot");
     __shared__ __attribute__((aligned(16))) uint32_t tk[kHotTable], tc[kHotTable];
     __shared__ unsigned long long best[kHotSlots];
     __shared__ __attribute__((aligned(16))) uint32_t skey[kHotSlots];
@@ -165,23 +166,26 @@ __global__ void __launch_bounds__(1024) hist_hot_kernel(const uint32_t *__restri
     }
     if (tid < kHotSlots) best[tid] = 0ull;
     __syncthreads();
-#pragma unroll 1
+    // First probes of all kPer samples issued together (one LDS round trip for the lot; the
+    // compare-and-swap claims an empty entry or returns its key), then the rare ones that met
+    // another key walk on one by one. kHotSamples < kHotTable: a free or matching entry is
+    // always found.
+    uint32_t hh[kPer], cur[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        hh[k] = (smp[k] * 0x85EBCA6Bu) >> (32 - 14);
+        cur[k] = smp[k] < num_bins ? atomicCAS(&tk[hh[k]], kNoKey, smp[k]) : smp[k];
+    }
+#pragma unroll
     for (int k = 0; k < kPer; ++k) {
         const uint32_t key = smp[k];
         if (key >= num_bins) continue;
-        uint32_t h = (key * 0x85EBCA6Bu) >> (32 - 14);
-        // kHotSamples < kHotTable: a free or matching entry is always found
-        for (int probe = 0; probe < kHotTable; ++probe) {
-            // a plain read first: a sampled key is mostly already there, and a compare-and-swap
-            // of many lanes on one hot key's entry serialises
-            uint32_t cur = tk[h];
-            if (cur == kNoKey) cur = atomicCAS(&tk[h], kNoKey, key);
-            if (cur == kNoKey || cur == key) {
-                atomicAdd(&tc[h], 1u);
-                break;
-            }
+        uint32_t h = hh[k], c = cur[k];
+        for (int probe = 0; probe < kHotTable && !(c == kNoKey || c == key); ++probe) {
             h = (h + 1) & (kHotTable - 1);
+            c = atomicCAS(&tk[h], kNoKey, key);
         }
+        atomicAdd(&tc[h], 1u);
     }
     __syncthreads();
     for (int i = tid; i < kHotTable / 4; i += 1024) {
@@ -196,19 +200,25 @@ __global__ void __launch_bounds__(1024) hist_hot_kernel(const uint32_t *__restri
     __syncthreads();
     // row position of slot i: the rank of its key among the valid keys (distinct; kNoKey sorts
     // last), empty slots after them in slot order (their place from the waves' ballots)
+    // (four threads per slot, a quarter of the entries each)
     if (tid < kHotSlots) {
-        const uint32_t key = skey[tid];
         const int lane = tid % kWave, wave = tid / kWave;
-        const uint64_t empty = __ballot(key == kNoKey);
+        const uint64_t empty = __ballot(skey[tid] == kNoKey);
         if (lane == 0) s_empty[wave] = (uint32_t)__builtin_popcountll(empty);
+        s_rank[tid] = 0;
+    }
+    __syncthreads();
+    {
+        const int slot = tid % kHotSlots, part = tid / kHotSlots;
+        const uint32_t key = skey[slot];
         uint32_t below = 0;
-        const uint4 *s4 = reinterpret_cast<const uint4 *>(skey);
-#pragma unroll 16
-        for (int q = 0; q < kHotSlots / 4; ++q) {
+        const uint4 *s4 = reinterpret_cast<const uint4 *>(skey) + part * (kHotSlots / 16);
+#pragma unroll
+        for (int q = 0; q < kHotSlots / 16; ++q) {
             const uint4 v = s4[q];
             below += (v.x < key ? 1u : 0u) + (v.y < key ? 1u : 0u) + (v.z < key ? 1u : 0u) + (v.w < key ? 1u : 0u);
         }
-        s_rank[tid] = below;
+        if (below) atomicAdd(&s_rank[slot], below);
     }
     __syncthreads();
     if (tid < kHotSlots) {

@@ -48,19 +48,19 @@ MODES = ("oblivious", "aware", "rotated")
 # launches. Atomic and random-access kernels move whole requests (a 16-byte CAS or probe
 # costs a request each way).
 TRAFFIC = {
-    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1311178197,
-    ("hash_2p26_lf0.5_u64", "warm", "aware"): 20176614578,
-    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 544988190,
-    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 544873978,
-    ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245928300,
-    ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3925162725,
-    ("bfs_rmat22_ef16", "warm", "aware"): 238931202,
-    ("gemv_f32_4096x4096", "warm", "aware"): 67718237,
-    ("gemv_f32_4096x4096", "cold", "aware"): 67720478,
-    ("gemv_f16_14336x4096", "warm", "aware"): 117650572,
-    ("gemv_f16_14336x4096", "cold", "aware"): 117651918,
-    ("gemv_f16_4096x14336", "warm", "aware"): 118182001,
-    ("gemv_f16_4096x14336", "cold", "aware"): 118188350,
+    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1311185290,
+    ("hash_2p26_lf0.5_u64", "warm", "aware"): 20177918445,
+    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 545198935,
+    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 544859537,
+    ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 244840050,
+    ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3925215361,
+    ("bfs_rmat22_ef16", "warm", "aware"): 238955381,
+    ("gemv_f32_4096x4096", "warm", "aware"): 67716891,
+    ("gemv_f32_4096x4096", "cold", "aware"): 67719502,
+    ("gemv_f16_14336x4096", "warm", "aware"): 117650590,
+    ("gemv_f16_14336x4096", "cold", "aware"): 117651916,
+    ("gemv_f16_4096x14336", "warm", "aware"): 118182314,
+    ("gemv_f16_4096x14336", "cold", "aware"): 118188052,
 }
 
 

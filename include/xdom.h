@@ -103,7 +103,11 @@ int xd_domain_scan(int num_wg, uint32_t *out_placement, void *stream);
  * (measured: near lines ~850 cycles from HBM / ~520 from the Infinity Cache, far lines
  * ~1070 / ~740). Same form as the reference's side prediction
  * predict_map_memory_attr_far (utility/latopt.cuh:255-263), with a fixed instead of a
- * per-page attribute. The home-routed kernels (hash, GEMV row segments) use this mask. */
+ * per-page attribute. The home-routed kernels (hash, GEMV row segments) use this mask when
+ * no page map is passed. Any non-zero mask of bits at or above 13 is accepted; one without
+ * bit 13 can put both 8 KiB chunks of a 16 KiB pair on one die, and the hash bulk build then
+ * takes its contiguous ranges instead of die halves (the other routes read every chunk once
+ * under any mask, near or not). */
 uint64_t xd_home_mask(void);
 int xd_set_home_mask(uint64_t mask);
 
@@ -364,9 +368,11 @@ int xd_hash_insert_u64(void *table, uint64_t slots, const uint64_t *keys, const 
  * 2^15 .. 2^30 slots are built range by range in LDS (4096 slots per range, two split passes,
  * plain stores, a compare-and-swap fix-up for the few pairs that run past a range's end);
  * XD_MODE_AWARE makes a range the 8 KiB chunks homed on one I/O die and builds it on that
- * die, XD_MODE_ROTATED on the other die. Other sizes and n = 0 are cleared and inserted
- * (xd_hash_init + xd_hash_insert_u64). The workspace (xd_hash_build_workspace_size, 0 for
- * those shapes; about 3.1 n x 16 bytes otherwise) needs no initial contents. */
+ * die, XD_MODE_ROTATED on the other die. Other sizes, n = 0 and calls of fewer than
+ * slots / 64 pairs are cleared and inserted (xd_hash_init + xd_hash_insert_u64). The
+ * workspace (xd_hash_build_workspace_size, 0 for those shapes) needs no initial contents; it
+ * is about 3.1 n x 16 bytes at load factors near 0.5 and at most about 7 n x 16 bytes (each
+ * range's regions have a floor of ~2 x 72 pairs plus 32 spill slots). */
 size_t xd_hash_build_workspace_size(uint64_t n, uint64_t slots);
 int xd_hash_build_u64(void *table, uint64_t slots, const uint64_t *keys, const uint64_t *vals, uint64_t n,
                       int mode, const uint8_t *home_attr, void *workspace, size_t workspace_bytes,

@@ -53,6 +53,7 @@ constexpr int kBuildLoad = 4;                       // pairs in flight per threa
 constexpr uint32_t kSpillPerRange = 32;  // expected ~0.25 per run end (two per aware range)
 constexpr int kMinLgSlots = 15;          // 8 ranges: one per XCD slot of a grid
 constexpr int kMaxLgSlots = 30;          // two digits of at most 9 bits
+constexpr uint64_t kMinPairsPerRange = 64;  // fewer pairs per range (load factor < 1/64): clear + insert
 constexpr int kBuildLdsPages = 4096;     // tables up to 8 GiB stage their page map in LDS
 constexpr int kFixThreads = 256;
 static_assert(kChunkSlots * 8 == kRange, "an aware range is one chunk of each of 8 pairs");
@@ -364,6 +365,10 @@ static BuildLayout build_layout(uint64_t n, uint64_t slots) {
     int lg = 0;
     while ((1ull << lg) < slots) ++lg;
     L.bulk = n > 0 && n < (1ull << 32) && lg >= kMinLgSlots && lg <= kMaxLgSlots && (1ull << lg) == slots;
+    // at least kMinPairsPerRange pairs per range on average: below that the regions' floor
+    // (64 + 1/32 + six deviations each) would size the workspace instead of n, and clearing
+    // plus inserting so few keys costs no more than the build's whole-table stores
+    L.bulk = L.bulk && n >= (uint64_t)kMinPairsPerRange << (lg - kLgRange);
     if (!L.bulk) return L;
     const int nrb = lg - kLgRange;
     L.dB = nrb / 2;
@@ -434,8 +439,13 @@ int xd_hash_build_u64(void *table, uint64_t slots, const uint64_t *keys, const u
     BuildGeom g;
     g.mask = slots - 1;
     g.base = base;
-    // die ranges need whole 16 KiB pairs of chunks at every 128 KiB region
-    g.die = (mode != XD_MODE_OBLIVIOUS && base % (2 * kHomeChunk) == 0) ? 1 : 0;
+    // Die ranges need whole 16 KiB pairs of chunks at every 128 KiB region, and one chunk of
+    // each pair on either die: true with a page map (the home flips with bit 13 inside a page)
+    // and with an address mask that holds bit 13. Under another mask both chunks of a pair
+    // can share a die, and the two would be built into one LDS run, so such calls take the
+    // contiguous ranges.
+    const bool pairs_split = home_attr != nullptr || (home_mask() & kHomeChunk) != 0;
+    g.die = (mode != XD_MODE_OBLIVIOUS && base % (2 * kHomeChunk) == 0 && pairs_split) ? 1 : 0;
     g.home = HomeMap{home_attr, base / kHomePage, home_mask()};
 
     const uint64_t nclear = (uint64_t)L.na + L.nr + 1;

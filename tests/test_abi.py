@@ -112,8 +112,9 @@ def test_probes_reject_bad_arguments():
 
 def test_hash_build_workspace_and_argument_checks():
     """The build's workspace query: 0 where the call clears and inserts (no pairs, tables
-    outside 2^15 .. 2^30 slots), about 3.1 x 16 n bytes otherwise and growing with n; bad
-    arguments are refused before any HIP call."""
+    outside 2^15 .. 2^30 slots, fewer than slots / 64 pairs), about 3.3 x 16 n bytes at load
+    factor 0.5, at most 7 x 16 n bytes, and growing with n; bad arguments are refused before
+    any HIP call."""
     from l2domain_amd import _lib
     lib = _lib.lib
     assert lib.xd_hash_build_workspace_size(0, 1 << 27) == 0
@@ -121,20 +122,27 @@ def test_hash_build_workspace_and_argument_checks():
     assert lib.xd_hash_build_workspace_size(1 << 20, 1 << 31) == 0
     big = lib.xd_hash_build_workspace_size(1 << 26, 1 << 27)
     assert 3.0 * 16 * (1 << 26) < big < 3.4 * 16 * (1 << 26)
-    sizes = [lib.xd_hash_build_workspace_size(n, 1 << 20) for n in (1, 1000, 100000, 500000)]
+    assert lib.xd_hash_build_workspace_size(1, 1 << 30) == 0  # (the ranges' floor no longer sizes it)
+    assert lib.xd_hash_build_workspace_size((1 << 14) - 1, 1 << 20) == 0
+    ns = (1 << 14, 100000, 500000)
+    sizes = [lib.xd_hash_build_workspace_size(n, 1 << 20) for n in ns]
     assert all(a < b for a, b in zip(sizes, sizes[1:])) and sizes[0] > 0
+    for n, slots in [(n, 1 << 20) for n in ns] + [(1 << 24, 1 << 30), (1 << 26, 1 << 27)]:
+        assert lib.xd_hash_build_workspace_size(n, slots) <= 7 * 16 * n, (n, slots)
     ws = (C.c_uint8 * 64)()
     fake = C.c_void_p(4096)  # never dereferenced: every call below fails its checks first
     keys = C.c_void_p(8192)
+    n = 2000  # >= slots / 64: the bulk path, whose workspace checks come before any HIP call
     cases = [
-        (None, 1 << 16, keys, keys, 10, 0, None, ws, 64),      # NULL table
-        (fake, 3 << 15, keys, keys, 10, 0, None, ws, 64),      # slots not a power of two
-        (fake, 1 << 16, None, keys, 10, 0, None, ws, 64),      # NULL keys
-        (fake, 1 << 16, keys, keys, 10, 7, None, ws, 64),      # bad mode
-        (fake, 1 << 16, C.c_void_p(8196), keys, 10, 0, None, ws, 64),  # keys not 8-byte aligned
-        (fake, 1 << 16, keys, keys, 10, 0, None, ws, 64),      # workspace smaller than the query
-        (fake, 1 << 16, keys, keys, 10, 0, None, None, 0),     # no workspace
+        (None, 1 << 16, keys, keys, n, 0, None, ws, 64),      # NULL table
+        (fake, 3 << 15, keys, keys, n, 0, None, ws, 64),      # slots not a power of two
+        (fake, 1 << 16, None, keys, n, 0, None, ws, 64),      # NULL keys
+        (fake, 1 << 16, keys, keys, n, 7, None, ws, 64),      # bad mode
+        (fake, 1 << 16, C.c_void_p(8196), keys, n, 0, None, ws, 64),  # keys not 8-byte aligned
+        (fake, 1 << 16, keys, keys, n, 0, None, ws, 64),      # workspace smaller than the query
+        (fake, 1 << 16, keys, keys, n, 0, None, None, 0),     # no workspace
     ]
+    assert lib.xd_hash_build_workspace_size(n, 1 << 16) > 64
     for table, slots, k, v, n, mode, home, w, wb in cases:
         rc = lib.xd_hash_build_u64(table, slots, k, v, n, mode, home, w, wb, None, None)
         assert rc in (_lib.XD_ERR_INVALID_ARG, _lib.XD_ERR_WORKSPACE), (slots, n, mode, rc)

@@ -27,6 +27,7 @@
 //      thread, units spread over the whole grid in every mode.
 #include <hip/hip_runtime.h>
 
+
 #include "xd_common.hpp"
 
 namespace xd {
@@ -82,7 +83,7 @@ struct HistBucket {
 
 struct HistLayout {
     int nb, ntiles, per_xcd, nitems;
-    size_t part, offs, tot, buckets, partials, hot, hot_part, total;
+    size_t part, offs, tot, buckets, partials, hot, hot_part, ones, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -116,6 +117,9 @@ static HistLayout hist_layout(size_t n, uint32_t num_bins) {
     o = align256(o + (size_t)kHotWords * sizeof(uint32_t));
     L.hot_part = o;
     o = align256(o + (size_t)L.ntiles * kHotSlots * sizeof(uint32_t));
+    // an 8 KiB chunk of all-ones keys (written by the sampling pass)
+    L.ones = o;
+    o = align256(o + kHomeChunk);
     L.total = o;
     return L;
 }
@@ -144,7 +148,7 @@ __device__ __forceinline__ uint32_t hot_slot(uint32_t key) { return key & (kHotS
 // function of the keys alone). Which keys are hot changes where they are counted, never the
 // counts. Needs n >= kHotSamples.
 __global__ void __launch_bounds__(1024) hist_hot_kernel(const uint32_t *__restrict__ keys, size_t n, uint32_t num_bins,
-                                                        int nb, uint32_t *__restrict__ hot) {
+                                                        int nb, uint32_t *__restrict__ hot, uint32_t *__restrict__ ones) {
     constexpr int kPer = kHotSamples / 1024;
     constexpr int kRun = kHotSamples / kHotBlocks;
     static_assert(1024 == 4 * kHotSlots, "the rank loop runs four threads per slot");
@@ -165,6 +169,8 @@ __global__ void __launch_bounds__(1024) hist_hot_kernel(const uint32_t *__restri
         reinterpret_cast<uint4 *>(tc)[i] = make_uint4(0, 0, 0, 0);
     }
     if (tid < kHotSlots) best[tid] = 0ull;
+    // the lean partition's stand-in for vectors past the end of a routed group
+    reinterpret_cast<uint2 *>(ones)[tid] = make_uint2(0xffffffffu, 0xffffffffu);
     __syncthreads();
     // First probes of all kPer samples issued together (one LDS round trip for the lot; the
     // compare-and-swap claims an empty entry or returns its key), then the rare ones that met
@@ -296,9 +302,6 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
     __shared__ uint32_t wsum[kP1Threads / kWave];
     __shared__ uint32_t s_total;
     __shared__ uint32_t s_hot, s_hotc;
-    // hot counters: copy c of slot i at s_cnt[c * (kHotSlots + 1) + i] (rows padded so that the
-    // copies of one slot sit in different banks)
-    __shared__ uint32_t s_tab[kHotSlots], s_cnt[(kHotSlots + 1) * kHotCopies];
     __shared__ __attribute__((aligned(16))) uint16_t stage[kTileKeys + 8];
     constexpr bool VEC = KIND != kPartRange;
     const int g = (int)blockIdx.x;
@@ -389,18 +392,6 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
                 kk[4 * j + c] = idx < src.r1 ? src.keys[idx] : 0xffffffffu;
             }
     }
-    // The hot-key table, loaded after the keys (its LDS store then waits for them too,
-    // which the vote below does anyway; loaded first, it put a round trip before them).
-    // (kinds that run in calls with a table: packed, and the range kind beside them, whose
-    // tiles write zero rows)
-    constexpr bool HOT = PACK || KIND == kPartRange;
-    uint32_t my_perm = 0;
-    if (HOT && hot != nullptr && tid < kHotSlots) {
-        s_tab[tid] = hot[kHotTab + tid];
-        my_perm = hot[kHotPerm + tid];
-#pragma unroll
-        for (int c = 0; c < kHotCopies; ++c) s_cnt[c * (kHotSlots + 1) + tid] = 0;
-    }
     // Heavy hitter: wave 0 votes the tile's most frequent key among kPeelCand candidates on
     // 256 samples (the first four keys of each lane); every thread then counts that key in a
     // register and makes it a spare, so it is neither staged nor written: under a skewed
@@ -408,9 +399,9 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
     // tile's {key, count} goes after its bucket offsets; the count pass adds it.
     if (VEC && wave == 0) {
         uint32_t b1 = kNoKey, c1 = 0;
-        // (no vote with a hot-key table, which holds the tile's top key too)
+        // (calls with a hot-key table run the lean kinds, which peel nothing)
 #pragma unroll 1
-        for (int j = 0; j < (hot == nullptr ? kPeelCand : 0); ++j) {
+        for (int j = 0; j < kPeelCand; ++j) {
             const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)kk[0], j);
             const uint32_t m = (kk[0] == c ? 1u : 0u) + (kk[1] == c ? 1u : 0u) + (kk[2] == c ? 1u : 0u) +
                                (kk[3] == c ? 1u : 0u);
@@ -439,27 +430,6 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
             }
             n1 = wave_sum_u32(n1);
             if (lane == 0 && n1) atomicAdd(&s_hotc, n1);
-        }
-        // keys of the hot table: counted in LDS and made spares (hot is null for calls that
-        // have no table; the unpacked kinds, at 64 registers already, never look up)
-        // (the table's keys are below num_bins, so a spare never matches; every read of a
-        // batch is issued before its adds, which the compiler cannot reorder past them)
-        if (PACK && hot != nullptr) {
-            constexpr int kBatch = 2 * kP1Vec;
-            uint32_t *my_cnt = s_cnt + (lane & (kHotCopies - 1)) * (kHotSlots + 1);
-#pragma unroll
-            for (int j0 = 0; j0 < 4 * kP1Vec; j0 += kBatch) {
-                uint32_t e[kBatch];
-#pragma unroll
-                for (int j = 0; j < kBatch; ++j) e[j] = s_tab[hot_slot(kk[j0 + j])];
-#pragma unroll
-                for (int j = 0; j < kBatch; ++j) {
-                    if (e[j] == kk[j0 + j]) {
-                        atomicAdd(&my_cnt[hot_slot(kk[j0 + j])], 1u);
-                        kk[j0 + j] = spare;
-                    }
-                }
-            }
         }
     }
 
@@ -551,12 +521,9 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
         // deals only to buckets with a non-zero total: one unit per peeling tile is enough
         if (VEC && h1 != kNoKey && s_hotc) atomicAdd(&my_tot[h1 >> kHB], 1u);
     }
-    if (HOT && hot != nullptr && tid < kHotSlots) {
-        uint32_t c = 0;
-#pragma unroll
-        for (int k = 0; k < kHotCopies; ++k) c += s_cnt[k * (kHotSlots + 1) + tid];
-        hot_part[(size_t)t * kHotSlots + my_perm] = c;
-    }
+    // In a call with a hot-key table (whose hot keys the lean kinds count) this kind's tiles
+    // add no hot counts: zero rows, as the count pass sums the rows of every tile.
+    if (hot != nullptr && tid < kHotSlots) hot_part[(size_t)t * kHotSlots + tid] = 0u;
 
     const uint32_t nvec = (tile_total + 7) / 8;  // 8 u16 per 16-byte store
     const uint4 *from = reinterpret_cast<const uint4 *>(stage);
@@ -567,9 +534,8 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
 // Two workgroups of 16 waves share a CU only while a wave holds at most 80 scalar registers
 // in all (measured: the routed packed kind at 82 ran at half the resident waves, 408 against
 // 286 us at 2^28 keys, though the compiler's occupancy estimate said 8 waves per SIMD), so
-// the packed kinds, which carry the hot-key lookups, are capped (78 requested gives 76 in
-// all; 74 gave 72 but spilled half again as many scalars to vector lanes); the unpacked ones
-// stay within 80 uncapped, and a cap would cost them a vector register past 64.
+// every partition kind is capped (78 requested gives 76 in all; 74 gave 72 but spilled half
+// again as many scalars to vector lanes).
 constexpr int kPartPackedSgprs = 78;
 
 template <int KIND>
@@ -581,10 +547,253 @@ hist_partition_packed_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *_
 }
 
 template <int KIND>
-__global__ void __launch_bounds__(kP1Threads)
+__global__ void __launch_bounds__(kP1Threads) __attribute__((amdgpu_num_sgpr(kPartPackedSgprs)))
 hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restrict__ part, uint32_t *__restrict__ offs,
                       uint32_t *__restrict__ tot, const uint32_t *__restrict__ hot, uint32_t *__restrict__ hot_part) {
     partition_tile<KIND, false>(src, num_bins, nb, part, offs, tot, hot, hot_part);
+}
+
+// ---------------------------------------------------------------------------------------
+// 1b. lean partition: calls with a hot-key table into at most kPackBuckets buckets
+// ---------------------------------------------------------------------------------------
+// The packed multi-split of partition_tile with the per-key work cut to what the split needs.
+// The generic kinds spend about 30 VALU instructions and 5 LDS instructions a key; the LDS
+// pipe then bounds the pass (dropping only the stage stores from a timing copy saved 31 us
+// of 236 at 2^28 keys; the key loads alone take 183 us).
+//  * a wave's 64 key vectors are consecutive (in a routed tile, inside one 8 KiB chunk), so
+//    their addresses are wave-uniform and computed with scalar instructions; a vector past
+//    the end of a routed group is loaded from an 8 KiB chunk of all-ones keys in the
+//    workspace instead, so no key carries a range flag;
+//  * one min() guards the range: bound = nb << kHB, so a key at or above it becomes `bound`,
+//    whose counter row (row nb) is the spare row; a key in [num_bins, bound) is split like any
+//    key of the last bucket, counted past num_bins by the count pass and dropped by the merge
+//    (which writes bins below num_bins only);
+//  * one returning LDS add per key: a hot key adds to its hot counter (lane % 8's copy), any
+//    other key to its counter column, and the hot key's returned value is dropped: it
+//    becomes a spare at slot `lane` of the spare row (the stage's trash);
+//  * a key's slot in its column is packed at bit kLeanShift, one above the key's bit 20, so
+//    x >> (kLeanShift - 1) is twice the slot: the stage byte address in one more op;
+//  * the stage has room past kTileKeys for every spare position, so the scatter needs no
+//    clamp, and it stores the packed register's low half as it is: bits 0-14 the in-bucket
+//    offset, bit 15 the bucket's low bit, which the count pass masks off in the same
+//    instruction that extracts the u16.
+constexpr int kLeanRows = kPackBuckets + 1;                    // bucket rows, then the spare row
+constexpr int kLeanCopyStride = kHotSlots + 1;                 // copies of one slot in different banks
+constexpr int kLeanColumnKeys = kP1Threads / kWave * 4 * kP1Vec;  // keys one counter column can take
+constexpr int kLeanStage = kTileKeys + kLeanColumnKeys;
+static_assert(kLeanStage % 8 == 0, "the stage is copied out in 16-byte vectors");
+static_assert(kLeanColumnKeys >= kWave, "a hot key's trash slot (its lane) is a spare position");
+constexpr int kLeanShift = 22;  // keys <= kPackSpare = 2^20: bit 21 stays clear
+static_assert(kPackSpare < (1u << (kLeanShift - 1)), "bit kLeanShift - 1 of a packed key is clear");
+static_assert(kLeanColumnKeys <= (1 << (32 - kLeanShift)), "packed slots overflow");
+static_assert(kLeanRows * kWave * 4 <= (0x3f00 | 0xff) + 1, "row offsets fit the 6-bit row field");
+
+struct LeanLds {
+    uint32_t col[kLeanRows * kWave];                // counter (row, lane), then each column's start
+    uint32_t cnt[kHotCopies * kLeanCopyStride];     // hot counters: copy c of slot i at c * stride + i
+    uint32_t tab[kHotSlots];                        // the hot-key table
+    uint32_t wsum[kP1Threads / kWave];
+    uint32_t total;
+    uint32_t pad_[3];
+    uint16_t stage[kLeanStage];
+};
+static_assert(offsetof(LeanLds, col) == 0, "counter byte offsets are offsets into the struct");
+static_assert(offsetof(LeanLds, stage) % 16 == 0, "stage copied out with 16-byte loads");
+
+template <int KIND>
+__global__ void __launch_bounds__(kP1Threads) __attribute__((amdgpu_num_sgpr(kPartPackedSgprs)))
+hist_partition_lean_kernel(PartSrc src, uint32_t bound, int nb, uint16_t *__restrict__ part,
+                           uint32_t *__restrict__ offs, uint32_t *__restrict__ tot, const uint32_t *__restrict__ hot,
+                           uint32_t *__restrict__ hot_part, const uint32_t *__restrict__ ones) {
+    __shared__ __attribute__((aligned(16))) LeanLds S;
+    const int g = (int)blockIdx.x;
+    const int tid = (int)threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    int t;
+    uint32_t want = 0;
+    int grp = 0;
+    if (KIND == kPartRouted) {
+        // as partition_tile: tile 2i + d is group i's chunks homed on die d
+        grp = (g / kNumXcd) * (kNumXcd / 2) + g % (kNumXcd / 2);
+        if (grp >= src.groups) return;
+        want = src.mode == XD_MODE_AWARE ? wg_die(g) : (wg_die(g) ^ 1u);
+        t = 2 * grp + (int)want;
+    } else {
+        t = src.tile0 + g;
+    }
+
+    uint32_t kk[4 * kP1Vec];
+    auto put = [&](int j, const uint4 &v) {
+        kk[4 * j] = v.x;
+        kk[4 * j + 1] = v.y;
+        kk[4 * j + 2] = v.z;
+        kk[4 * j + 3] = v.w;
+    };
+    if (KIND == kPartFull) {
+        // keys + r0 is 16-byte aligned; only the launch's last tile can be partial
+        const uint4 *kv = reinterpret_cast<const uint4 *>(src.keys + src.r0) + (size_t)g * (kTileKeys / 4);
+        const size_t left = (src.r1 - src.r0) / 4 - (size_t)g * (kTileKeys / 4);  // vectors from this tile on
+        if (left >= (size_t)(kTileKeys / 4)) {
+#pragma unroll
+            for (int j = 0; j < kP1Vec; ++j) put(j, load_stream(kv + tid + j * kP1Threads));
+        } else {
+            // (uniform branch) a vector past the end reads the all-ones chunk, whose keys the
+            // guard turns into spares
+#pragma unroll
+            for (int j = 0; j < kP1Vec; ++j) {
+                const uint32_t v = (uint32_t)(tid + j * kP1Threads);
+                put(j, load_stream(v < left ? kv + v : reinterpret_cast<const uint4 *>(ones) + ((uint32_t)tid & 511u)));
+            }
+        }
+    } else {
+        // Routed: vector tid + j * kP1Threads of the tile is vector tid % 512 of the chunk of
+        // pair 2j + tid / 512 of the group; tid / 512 = wave / 8, so the chunk is wave-uniform.
+        // The group spans at most kRouteGroupPairs * 16 KiB <= 2 MiB, so at most two map pages:
+        // the even chunk of a pair has address bit 13 clear, so its home is its page's.
+        const uint64_t A = reinterpret_cast<uint64_t>(src.keys);
+        const uint64_t P0 = src.pair_first + (uint64_t)grp * kRouteGroupPairs;
+        const uint32_t np = (uint32_t)min((uint64_t)kRouteGroupPairs, src.npairs - (uint64_t)grp * kRouteGroupPairs);
+        const uint64_t pg_lo = (P0 * 16384) / kHomePage;
+        const uint64_t pg_hi = ((P0 + np) * 16384 - 1) / kHomePage;
+        uint32_t h_lo, h_hi;
+        if (src.home.attr) {
+            h_lo = __builtin_amdgcn_readfirstlane((uint32_t)src.home.attr[pg_lo - src.home.page0]);
+            h_hi = __builtin_amdgcn_readfirstlane((uint32_t)src.home.attr[pg_hi - src.home.page0]);
+        } else {
+            h_lo = home_of(pg_lo * kHomePage, src.home.mask);
+            h_hi = home_of(pg_hi * kHomePage, src.home.mask);
+        }
+        const uint32_t lv = (uint32_t)tid & 511u;
+#pragma unroll
+        for (int j = 0; j < kP1Vec; ++j) {
+            const uint32_t pi = (uint32_t)(2 * j + wave / 8);
+            const uint64_t P = P0 + min(pi, np - 1u);
+            const uint32_t h0 = (P * 16384) / kHomePage == pg_lo ? h_lo : h_hi;
+            // (chunk addresses as offsets from the keys pointer: a global pointer, not flat)
+            const uint32_t *chunk = src.keys + ((2 * P + (h0 ^ want)) * kHomeChunk - A) / 4;
+            const uint32_t *base = pi < np ? chunk : ones;
+            put(j, load_stream(reinterpret_cast<const uint4 *>(base) + lv));
+        }
+    }
+
+    // counters zeroed and the table copied in after the loads are issued
+    for (int i = tid; i < kLeanRows * kWave; i += kP1Threads) S.col[i] = 0;
+    for (int i = tid; i < kHotCopies * kLeanCopyStride; i += kP1Threads) S.cnt[i] = 0;
+    uint32_t my_perm = 0;
+    if (tid < kHotSlots) {
+        S.tab[tid] = hot[kHotTab + tid];
+        my_perm = hot[kHotPerm + tid];
+    }
+#pragma unroll
+    for (int j = 0; j < 4 * kP1Vec; ++j) kk[j] = min(kk[j], bound);
+    __syncthreads();
+
+    // One returning add per key (byte offsets into S): a hot key's counter copy, else the key's
+    // counter column (row key >> kHB, at most the spare row, column = lane). Table keys are
+    // below num_bins <= bound and empty entries are all ones, so a spare never matches.
+    const uint32_t lanebyte = (uint32_t)lane * 4u;
+    const uint32_t hotbase =
+        (uint32_t)offsetof(LeanLds, cnt) + (uint32_t)(lane & (kHotCopies - 1)) * kLeanCopyStride * 4u;
+    const uint32_t hotspare = bound | ((uint32_t)lane << kLeanShift);  // trash slot `lane` of the spare row
+    char *const sb = reinterpret_cast<char *>(&S);
+    auto col_off = [&](uint32_t x) { return ((x >> (kHB - 8)) & 0x3f00u) | lanebyte; };
+    constexpr int kBatch = 2 * kP1Vec;
+#pragma unroll
+    for (int j0 = 0; j0 < 4 * kP1Vec; j0 += kBatch) {
+        uint32_t e[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) e[j] = S.tab[hot_slot(kk[j0 + j])];
+        // the batch's offsets, then its adds back to back, then the packing (a hot offset is at
+        // or above offsetof(cnt), every column offset below it)
+        uint32_t off[kBatch], pos[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const uint32_t k = kk[j0 + j];
+            // both offsets computed, then one select (the compiler otherwise branches per key)
+            uint32_t ho = hotbase + 4u * hot_slot(k), co = col_off(k);
+            asm("" : "+v"(ho), "+v"(co));
+            off[j] = e[j] == k ? ho : co;
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) pos[j] = atomicAdd(reinterpret_cast<uint32_t *>(sb + off[j]), 1u);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const uint32_t k = kk[j0 + j];
+            kk[j0 + j] = off[j] >= (uint32_t)offsetof(LeanLds, cnt) ? hotspare : (k | (pos[j] << kLeanShift));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 4 * kP1Vec; ++j) asm volatile("" : "+v"(kk[j]));
+    __syncthreads();
+
+    // exclusive scan of the nb * 64 counters in (bucket, column) order, two per thread
+    const int ncol = nb * kWave;
+    const int i0 = 2 * tid;
+    const uint32_t c0 = i0 < ncol ? S.col[i0] : 0u;
+    const uint32_t c1 = i0 + 1 < ncol ? S.col[i0 + 1] : 0u;
+    const uint32_t v = c0 + c1;
+    const uint32_t incl = wave_incl_scan_u32(v);
+    if (lane == kWave - 1) S.wsum[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+        const uint32_t w = lane < kP1Threads / kWave ? S.wsum[lane] : 0u;
+        const uint32_t wi = wave_incl_scan_u32(w);
+        if (lane < kP1Threads / kWave) S.wsum[lane] = wi - w;
+        if (lane == kP1Threads / kWave - 1) S.total = wi;
+    }
+    __syncthreads();
+    {
+        const uint32_t e = S.wsum[wave] + incl - v;
+        if (i0 < ncol) S.col[i0] = e;
+        if (i0 + 1 < ncol) S.col[i0 + 1] = e + c0;
+    }
+    if (tid < kWave) S.col[nb * kWave + tid] = kTileKeys;  // the spare row's keys land past kTileKeys
+    __syncthreads();
+
+    // Scatter in batches: the column starts first, then the stores, hot keys' left out (their
+    // trash stores shared dwords and cost bank cycles: 6.8 against 4.4 cycles per wave store
+    // in a bank simulation of Zipf tiles)
+#pragma unroll
+    for (int j0 = 0; j0 < 4 * kP1Vec; j0 += kBatch) {
+        uint32_t start[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) start[j] = *reinterpret_cast<const uint32_t *>(sb + col_off(kk[j0 + j]));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const uint32_t x = kk[j0 + j];
+            const uint32_t byte = 2u * start[j] + (x >> (kLeanShift - 1));  // 2 (start + slot)
+            if (x != hotspare) *reinterpret_cast<uint16_t *>(reinterpret_cast<char *>(S.stage) + byte) = (uint16_t)x;
+        }
+    }
+    __syncthreads();
+
+    const uint32_t tile_total = S.total;
+    uint32_t *my_offs = offs + (size_t)t * (nb + 1 + kPeelWords);
+    uint32_t *my_tot = tot + (size_t)(t % kNumXcd) * nb;
+    for (int b = tid; b < nb; b += kP1Threads) {
+        const uint32_t start = S.col[b * kWave];
+        const uint32_t end = b + 1 < nb ? S.col[(b + 1) * kWave] : tile_total;
+        my_offs[b] = start;
+        if (end > start) atomicAdd(&my_tot[b], end - start);
+    }
+    if (tid == 0) {
+        my_offs[nb] = tile_total;
+        my_offs[nb + 1] = kNoKey;  // nothing peeled
+        my_offs[nb + 2] = 0u;
+    }
+    if (tid < kHotSlots) {
+        uint32_t c = 0;
+#pragma unroll
+        for (int k = 0; k < kHotCopies; ++k) c += S.cnt[k * kLeanCopyStride + tid];
+        hot_part[(size_t)t * kHotSlots + my_perm] = c;
+    }
+    const uint32_t nvec = (tile_total + 7) / 8;
+    const uint4 *from = reinterpret_cast<const uint4 *>(S.stage);
+    uint4 *dst = reinterpret_cast<uint4 *>(part + (size_t)t * kTileKeys);
+    for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) dst[i] = from[i];
 }
 
 // ---------------------------------------------------------------------------------------
@@ -666,7 +875,8 @@ __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t 
     const uint32_t len = e0 - s0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        uint32_t key = (k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu);
+        // (15 bits: the lean partition leaves its bucket's low bit in bit 15)
+        uint32_t key = (k & 1) ? ((w[k >> 1] >> 16) & (kBucketBins - 1)) : (w[k >> 1] & (kBucketBins - 1));
         key = (e + (uint32_t)k - s0 < len) ? key : trash;
         if (VOTE) {
             const bool h1 = key == hot, h2 = key == hot2;  // a trash slot is never a hot key
@@ -821,7 +1031,7 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
             // (skipped after a hot-key table took the popular keys out of the runs: the votes
             // then rarely adopt a key and cost 7 us of the 105 at 2^28 Zipf keys)
             const bool sv = ea - sa < xa - sa;
-            const uint32_t sk = qa.x & 0xffffu;
+            const uint32_t sk = qa.x & (kBucketBins - 1);
             if (hot_tab == nullptr) {
             if (__builtin_popcountll(__ballot(sv && sk == hot)) < kWave / 4) {
                 const uint64_t svm = __ballot(sv);
@@ -1008,12 +1218,24 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     uint32_t *hot_part = reinterpret_cast<uint32_t *>(ws + L.hot_part);
     if (n >= kHotMinKeys && pack) {
         hot = reinterpret_cast<uint32_t *>(ws + L.hot);
-        launch("hist_hot_kernel", hist_hot_kernel, dim3(1), dim3(1024), 0, s, keys, n, num_bins, L.nb, hot);
+        launch("hist_hot_kernel", hist_hot_kernel, dim3(1), dim3(1024), 0, s, keys, n, num_bins, L.nb, hot,
+               reinterpret_cast<uint32_t *>(ws + L.ones));
         if (int rc = launch_status("hist_hot_kernel")) return rc;
     }
     using PartKernel = void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *, const uint32_t *, uint32_t *);
+    using LeanKernel =
+        void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *, const uint32_t *, uint32_t *, const uint32_t *);
     for (int k = 0; k < nplan; ++k) {
         const PartLaunch &pl = plan[k];
+        if (hot != nullptr && pl.kind != kPartRange) {
+            // the lean kinds: a hot-key table and at most kPackBuckets buckets
+            const LeanKernel lk =
+                pl.kind == kPartRouted ? hist_partition_lean_kernel<kPartRouted> : hist_partition_lean_kernel<kPartFull>;
+            launch("hist_partition_kernel", lk, dim3(pl.grid), dim3(kP1Threads), 0, s, pl.ps, (uint32_t)L.nb << kHB,
+                   L.nb, part, offs, tot, (const uint32_t *)hot, hot_part, (const uint32_t *)(ws + L.ones));
+            if (int rc = launch_status("hist_partition_kernel")) return rc;
+            continue;
+        }
         PartKernel kern;
         if (pl.kind == kPartRouted)
             kern = pack ? hist_partition_packed_kernel<kPartRouted> : hist_partition_kernel<kPartRouted>;

@@ -111,6 +111,10 @@ def _hot_case_keys(case: str) -> tuple[np.ndarray, int]:
         return rng.integers(0, 1100, size=n).astype(np.uint32), 1000
     if case == "one_key":
         return np.full(n, 123457, dtype=np.uint32), 1 << 20
+    if case == "bucket_multiple":  # 2^19 bins (16 whole buckets): half the keys past them, some far past
+        k = gen.zipf_keys_device(n, 1 << 20, 79, ZIPF_S).cpu().numpy().view(np.uint32).copy()
+        k[rng.integers(0, n, size=n // 64)] = rng.integers(1 << 20, 1 << 32, size=n // 64, dtype=np.uint64)
+        return k, 1 << 19
     if case == "same_low_byte":   # 4096 popular keys, all multiples of 256: one hot-table slot
         return (rng.zipf(1.3, size=n) % 4096 * 256).astype(np.uint32), 1 << 20
     raise ValueError(case)
@@ -118,7 +122,7 @@ def _hot_case_keys(case: str) -> tuple[np.ndarray, int]:
 
 @pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("case", ["zipf_identity", "zipf_scrambled", "one_bucket", "few_bins", "one_key",
-                                  "same_low_byte"])
+                                  "same_low_byte", "bucket_multiple"])
 def test_hot_table_cases(case, mode):
     keys, num_bins = _hot_case_keys(case)
     ref, _ = ora.histogram(keys, num_bins, nthreads=16)

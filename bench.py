@@ -47,6 +47,7 @@ MODES = ("oblivious", "aware", "rotated")
 # copy reads 2.000x what FETCH_SIZE counts, WRITE_SIZE 1.000x), summed over a step's
 # launches. Atomic and random-access kernels move whole requests (a 16-byte CAS or probe
 # costs a request each way).
+TRAFFIC_SRC = "profiles/traffic_by_config.md (FETCH_SIZE/WRITE_SIZE runs of the commit named there)"
 TRAFFIC = {
     ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1311185290,
     ("hash_2p26_lf0.5_u64", "warm", "aware"): 20177918445,
@@ -94,6 +95,7 @@ def timed_loop(fn, min_s: float, max_reps: int = 1 << 30) -> tuple[float, int]:
 # ---------------------------------------------------------------------------------------
 class Workload:
     single_kernel = False  # a step is exactly one launch
+    min_steps = 1          # timed steps at least (configs[0]: "single call plus 100 timed repeats")
     ic_resident = False    # warm data fits the 256 MB Infinity Cache
     cpu_parallel = True    # the CPU restatement has a multi-threaded form
     roof_bytes = 0         # algorithmic bytes per launch of the roofline kernel(s)
@@ -112,6 +114,7 @@ class GemvF32(Workload):
     unit = "GB/s"
     dtype = "f32"
     ic_resident = True
+    min_steps = 100  # a single call (the verification) plus 100 timed repeats, whatever --steps is
 
     def __init__(self, M=4096, K=4096):
         import numpy as np
@@ -222,9 +225,12 @@ class Hist(Workload):
         self.h = Histogram(n, num_bins)
         self.counts = torch.empty(num_bins, dtype=torch.int32, device="cuda")
         torch.cuda.synchronize()
-        # algorithmic bytes: 4 B per key read + 4 B per counter written
+        # algorithmic bytes of the step: 4 B per key read + 4 B per counter written
+        # (1,077,936,128 at the config); the roofline kernel, the partition pass, reads the keys
+        # (4 B per key) and never touches the counters, which the merge writes
         self.bytes = 4 * n + 4 * num_bins
-        self.roof_bytes = 4 * n  # the partition pass reads every key once
+        self.roof_bytes = 4 * n
+        self.roof_basis = "keys read by the partition pass (4 B per key); the counters are written by the merge"
 
     def step(self, mode):
         self.h(self.keys, self.counts, mode=mode, home_attr=self.home)
@@ -653,6 +659,7 @@ def run_workload(name, steps, warmup, cold=False, modes=MODES, cpu=True, cpu_bud
     import torch
     from l2domain_amd.domain import CacheFlusher
     wl = WORKLOADS[name]()
+    steps = max(steps, wl.min_steps)
     ok = wl.verify() if verify else None
     flusher = CacheFlusher() if cold else None
     # The first ~30 steps of a process run up to 20 % slower than the steady state; warming
@@ -666,11 +673,13 @@ def run_workload(name, steps, warmup, cold=False, modes=MODES, cpu=True, cpu_bud
     torch.cuda.synchronize()
     kt = {m: kernel_times(wl, m, steps, flusher) for m in modes}
     roof_s = {m: sum(v[0] for k, v in kt[m].items() if k in wl.roof_kernels(m)) for m in modes}
-    step_kernel_s = {m: sum(v[0] for v in kt[m].values()) for m in modes}
-    # cold steps: the kernels' own durations (the flush and the dispatch gaps are not the step)
-    tput_s = step_kernel_s if cold else sec
+    # Throughput from the event pair around each step, cold ones included: after the flush, an
+    # event, the step's launches, an event (as the reference times a cold call,
+    # gemv_cublas_benchmark.cu:84-90), so a step of two launches pays the gap between them.
+    # The kernels' own summed durations stay in the detail (ms_per_step_kernels).
+    tput_s = sec
     out = {"workload": wl, "verified": ok, "sec": sec, "tput_s": tput_s, "roof_s": roof_s, "kernels": kt,
-           "tput": {m: wl.throughput(tput_s[m]) for m in modes}}
+           "tput": {m: wl.throughput(tput_s[m]) for m in modes}, "steps": steps}
     if not cold and wl.ic_resident:
         out["ic_peak"] = ic_peak(wl, steps)
     if cpu:
@@ -697,16 +706,20 @@ def roofline(r, mode="aware", cold=False):
         bound, peak = "hbm", HBM_PEAK_GBS
     name = getattr(wl, "name", "")
     traffic = TRAFFIC.get((name, "cold" if cold else "warm", mode))
-    return {"bound": bound, "achieved": round(achieved, 1), "peak": round(peak, 1), "unit": "GB/s",
-            "frac": round(achieved / peak, 4), "traffic": traffic,
-            "kernel": "+".join(k for k in r["kernels"][mode] if k in wl.roof_kernels(mode)),
-            "kernel_us": round(sec * 1e6, 3), "bytes": wl.roof_bytes}
+    out = {"bound": bound, "achieved": round(achieved, 1), "peak": round(peak, 1), "unit": "GB/s",
+           "frac": round(achieved / peak, 4), "traffic": traffic,
+           "traffic_src": TRAFFIC_SRC if traffic is not None else None,
+           "kernel": "+".join(k for k in r["kernels"][mode] if k in wl.roof_kernels(mode)),
+           "kernel_us": round(sec * 1e6, 3), "bytes": wl.roof_bytes}
+    if getattr(wl, "roof_basis", None):
+        out["bytes_basis"] = wl.roof_basis
+    return out
 
 
 def compact(r, cold):
     """One short entry per configuration (the driver keeps only the tail of the line)."""
     t = r["tput"]
-    e = {"ok": r["verified"], "unit": r["workload"].unit}
+    e = {"ok": r["verified"], "unit": r["workload"].unit, "steps": r["steps"]}
     for m, k in (("aware", "aware"), ("oblivious", "obl"), ("rotated", "rot")):
         if m in t:
             e[k] = round(t[m], 2)
@@ -778,7 +791,7 @@ def main():
         "value": round(r["tput"][head], 3),
         "unit": wl.unit,
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": r["steps"],
         "warmup": args.warmup,
         "ms_per_step": round(sec * 1e3, 6),
         "higher_is_better": True,
@@ -795,6 +808,11 @@ def main():
         line["speedup_rotated_vs_oblivious"] = round(r["tput_s"]["oblivious"] / r["tput_s"]["rotated"], 4)
     line["modes"] = {m: round(v, 3) for m, v in r["tput"].items()}
     line["roofline"] = roofline(r, head, args.cold)
+    if getattr(wl, "bytes", 0) and wl.bytes != wl.roof_bytes:
+        # the whole step against the same peak: every algorithmic byte over the step's time
+        st = wl.bytes / sec / 1e9
+        line["roofline"]["step"] = {"bytes": wl.bytes, "achieved": round(st, 1),
+                                    "frac": round(st / line["roofline"]["peak"], 4)}
     line["cpu_baseline"] = r.get("cpu")
     details = {f"{args.workload}_{'cold' if args.cold else 'warm'}": detail(r, args.cold)}
     if not args.only:

@@ -292,34 +292,104 @@ gemv_seghome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, fl
     const int wave = (int)threadIdx.x / kWave;
     const int lane = (int)threadIdx.x % kWave;
     const int nv = S * kSegVec;
-    for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
-    __syncthreads();
+    // x is staged after the first A loads are issued (before them it put a round trip ahead
+    // of the stream, which a cold call pays in full)
+    auto stage_x = [&] {
+        for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
+        __syncthreads();
+    };
     const uint64_t abase = reinterpret_cast<uint64_t>(A);
     const int nseg = M * S;
     const int ngroups = (nseg + kGroup - 1) / kGroup;
+    // one segment j: loaded, reduced, met (the general path)
+    auto one_segment = [&](int j) {
+        const int row = j / S;
+        const int seg = j - row * S;
+        const uint4 *p = A + (size_t)j * kSegVec + lane;
+        uint4 a[CW];
+#pragma unroll
+        for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
+        const uint4 *xv = xs + seg * kSegVec + lane;
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int u = 0; u < CW; u += 2) {
+            acc0 = F16 ? dot16_f16(a[u], xv[u * kWave], acc0) : dot16_f32(a[u], xv[u * kWave], acc0);
+            acc1 = F16 ? dot16_f16(a[u + 1], xv[(u + 1) * kWave], acc1) : dot16_f32(a[u + 1], xv[(u + 1) * kWave], acc1);
+        }
+        const float part = wave_sum_f32(acc0 + acc1);
+        if (lane == 0) seg_meet<F16, PAIR>(part, j, row, seg, S, y, cnt, slot);
+    };
+    if (PAIR) {
+        // Rows of two segments: a group of 8 segments holds 4 rows, each with one segment on
+        // either die when the home function splits every 16 KiB pair (page map, or a mask with
+        // bit 13), so each of the 4 waves takes one wanted segment of a group. A wave takes its
+        // segments of two groups at once: both segments' loads in flight, both reduced, then
+        // both exchanges in one instruction (lanes 0 and 1). An exchange after every segment
+        // (the returning atomic waits for every load issued before it) held the second
+        // segment's loads back by a memory round trip. A wave's second segment of a group
+        // (other home functions) takes the general path.
+        const uint4 *xv = xs + lane;
+        bool staged = false;
+        for (int g0 = rank; g0 < ngroups || !staged; g0 += 2 * per_die) {
+            int jj[2], extra[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int g = g0 + t * per_die;
+                const int jl = g * kGroup + lane;
+                const bool wanted = g < ngroups && lane < kGroup && jl < nseg &&
+                                    home(abase + (uint64_t)jl * kHomeChunk) == want;
+                uint64_t m = __ballot(wanted);
+                for (int k = 0; k < wave && m; ++k) m &= m - 1;
+                jj[t] = m ? g * kGroup + __builtin_ctzll(m) : -1;  // (wave-uniform)
+                for (int k = 0; k < kGemvWaves && m; ++k) m &= m - 1;
+                extra[t] = m ? g * kGroup + __builtin_ctzll(m) : -1;  // at most one more: 8 per group
+            }
+            uint4 a[2][CW];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint4 *p = A + (size_t)(jj[t] >= 0 ? jj[t] : 0) * kSegVec + lane;  // (clamped: no load under a branch)
+#pragma unroll
+                for (int u = 0; u < CW; ++u) a[t][u] = p[u * kWave];
+            }
+            if (!staged) {  // (uniform over the workgroup: the first pass of every wave)
+                stage_x();
+                staged = true;
+                if (g0 >= ngroups) break;  // a workgroup with no groups only joined the barrier
+            }
+            float part[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint4 *xt = xv + (jj[t] >= 0 ? jj[t] % S : 0) * kSegVec;
+                float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+                for (int u = 0; u < CW; u += 2) {
+                    acc0 = F16 ? dot16_f16(a[t][u], xt[u * kWave], acc0) : dot16_f32(a[t][u], xt[u * kWave], acc0);
+                    acc1 = F16 ? dot16_f16(a[t][u + 1], xt[(u + 1) * kWave], acc1)
+                               : dot16_f32(a[t][u + 1], xt[(u + 1) * kWave], acc1);
+                }
+                part[t] = wave_sum_f32(acc0 + acc1);
+            }
+            // lane t meets segment jj[t]: the exact kernel's bits (p0 + p1, in segment order)
+            const int jm = lane == 0 ? jj[0] : jj[1];
+            if (lane < 2 && jm >= 0) {
+                const float pm = lane == 0 ? part[0] : part[1];
+                const int row = jm / S, seg = jm - row * S;
+                seg_meet<F16, true>(pm, jm, row, seg, S, y, cnt, slot);
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                if (extra[t] >= 0) one_segment(extra[t]);  // (wave-uniform)
+        }
+        return;
+    }
+    stage_x();
     for (int g = rank; g < ngroups; g += per_die) {
         const int jl = g * kGroup + lane;
         const bool wanted = lane < kGroup && jl < nseg && home(abase + (uint64_t)jl * kHomeChunk) == want;
         uint64_t m = __ballot(wanted);
         for (int k = 0; k < wave && m; ++k) m &= m - 1;
         while (m) {
-            const int j = g * kGroup + __builtin_ctzll(m);
-            const int row = j / S;
-            const int seg = j - row * S;
-            const uint4 *p = A + (size_t)j * kSegVec + lane;
-            uint4 a[CW];
-#pragma unroll
-            for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
-            const uint4 *xv = xs + seg * kSegVec + lane;
-            float acc0 = 0.0f, acc1 = 0.0f;
-#pragma unroll
-            for (int u = 0; u < CW; u += 2) {
-                acc0 = F16 ? dot16_f16(a[u], xv[u * kWave], acc0) : dot16_f32(a[u], xv[u * kWave], acc0);
-                acc1 = F16 ? dot16_f16(a[u + 1], xv[(u + 1) * kWave], acc1)
-                           : dot16_f32(a[u + 1], xv[(u + 1) * kWave], acc1);
-            }
-            const float part = wave_sum_f32(acc0 + acc1);
-            if (lane == 0) seg_meet<F16, PAIR>(part, j, row, seg, S, y, cnt, slot);
+            one_segment(g * kGroup + __builtin_ctzll(m));
             for (int k = 0; k < kGemvWaves && m; ++k) m &= m - 1;
         }
     }
@@ -352,8 +422,6 @@ gemv_chunkhome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, 
     const int lane = (int)threadIdx.x % kWave;
     const int P = (Hh + 1) / 2;
     const int nv = Hh * kHalfVec;
-    for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
-    __syncthreads();
     const uint64_t abase = reinterpret_cast<uint64_t>(A);
     const long long c0 = (long long)(abase / kHomeChunk);  // absolute chunk of A's first byte
     const long long nchunk = (long long)M * Hh / 2;
@@ -374,6 +442,10 @@ gemv_chunkhome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, 
 #pragma unroll
         for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
     }
+    // x staged after the first chunk's loads are issued (before them it put a round trip
+    // ahead of the stream, which a cold call pays in full)
+    for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
+    __syncthreads();
     for (; k < nq; k += step) {
         // pieces of the current chunk (r0 == r1: one piece of one row)
         const long long h0 = 2 * (c >= 0 ? c : 0);
@@ -515,10 +587,11 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         workspace_bytes >= (size_t)M * (size_t)(P + 1) * 4 && (reinterpret_cast<uintptr_t>(workspace) % 8) == 0) {
         const HomeMap home{home_attr, reinterpret_cast<uint64_t>(A) / kHomePage, home_mask()};
         float *part = reinterpret_cast<float *>(workspace);
-        // about eight pairs (one chunk each) per wave, measured best of 1, 2, 4, 8 and 16 at
-        // 4096 x 14336 fp16 (XD_GEMV_CHUNK_PAIRS_PER_WAVE overrides it for tuning sweeps)
+        // about four pairs (one chunk each) per wave: at 4096 x 14336 fp16 the chunk kernel
+        // took 19.8 / 16.3 / 15.6 / 15.9 us warm and 26.6 / 23.1 / 23.2 / 24.0 us cold at 1, 2,
+        // 4, 8 pairs (XD_GEMV_CHUNK_PAIRS_PER_WAVE overrides it for tuning sweeps)
         const long long npairs = (long long)M * Hh / 4 + 2;
-        long long ppw = 8;
+        long long ppw = 4;
         if (const char *e = getenv("XD_GEMV_CHUNK_PAIRS_PER_WAVE"))
             if (atoll(e) >= 1) ppw = atoll(e);
         long long cgrid = (npairs + 4 * ppw - 1) / (4 * ppw) * 2;

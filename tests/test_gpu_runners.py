@@ -57,10 +57,16 @@ def test_gemv_runner_reference_inputs(init):
         assert max(errs) == 0.0  # integer-valued inputs: every summation order is exact
 
 
-def test_gemv_vendor_runner():
-    rc, out, err = run("xd_gemv_vendor_run", 2048, 1024, 5, 1, 1)
+@pytest.mark.parametrize("inputs,shape", [("mix32", (2048, 1024)), ("f32", (4096, 4096)), ("f16", (14336, 4096)),
+                                          ("f16", (4096, 14336))])
+def test_gemv_vendor_runner(inputs, shape):
+    """rocBLAS sgemv on the reference's inputs and on the fp32 configuration, and its
+    mixed-precision gemv (fp16 in, fp32 accumulate and out) on both fp16 shapes; the runner
+    checks the result itself (exit 3 on a mismatch)."""
+    rc, out, err = run("xd_gemv_vendor_run", *shape, 5, 1, 1, inputs)
     assert rc == 0, out + err
     assert float(first_field(out, "cublas_ms")) > 0 and "vendor=rocblas" in out
+    assert f"inputs={inputs}" in out
 
 
 @pytest.mark.parametrize("args", [("--workload=zipf", 16, 2, 256, 1, 0, 1 << 20, 1.1, 1373), (32, 2, 128, 1, 0)])

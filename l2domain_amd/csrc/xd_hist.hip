@@ -521,9 +521,10 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
         // deals only to buckets with a non-zero total: one unit per peeling tile is enough
         if (VEC && h1 != kNoKey && s_hotc) atomicAdd(&my_tot[h1 >> kHB], 1u);
     }
-    // In a call with a hot-key table (whose hot keys the lean kinds count) this kind's tiles
-    // add no hot counts: zero rows, as the count pass sums the rows of every tile.
-    if (hot != nullptr && tid < kHotSlots) hot_part[(size_t)t * kHotSlots + tid] = 0u;
+    // The range kind runs beside the lean kinds in calls with a hot-key table (the keys before
+    // and after the vector tiles): its tiles add no hot counts, so their rows are zero, as the
+    // count pass sums the rows of every tile. (The other generic kinds run without a table.)
+    if (KIND == kPartRange && hot != nullptr && tid < kHotSlots) hot_part[(size_t)t * kHotSlots + tid] = 0u;
 
     const uint32_t nvec = (tile_total + 7) / 8;  // 8 u16 per 16-byte store
     const uint4 *from = reinterpret_cast<const uint4 *>(stage);
@@ -534,8 +535,9 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
 // Two workgroups of 16 waves share a CU only while a wave holds at most 80 scalar registers
 // in all (measured: the routed packed kind at 82 ran at half the resident waves, 408 against
 // 286 us at 2^28 keys, though the compiler's occupancy estimate said 8 waves per SIMD), so
-// every partition kind is capped (78 requested gives 76 in all; 74 gave 72 but spilled half
-// again as many scalars to vector lanes).
+// the packed and lean kinds are capped (78 requested gives 76 in all; 74 gave 72 but spilled
+// half again as many scalars to vector lanes); the unpacked ones stay within 80 uncapped, and
+// a cap would cost them a vector register past 64.
 constexpr int kPartPackedSgprs = 78;
 
 template <int KIND>
@@ -547,7 +549,7 @@ hist_partition_packed_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *_
 }
 
 template <int KIND>
-__global__ void __launch_bounds__(kP1Threads) __attribute__((amdgpu_num_sgpr(kPartPackedSgprs)))
+__global__ void __launch_bounds__(kP1Threads)
 hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restrict__ part, uint32_t *__restrict__ offs,
                       uint32_t *__restrict__ tot, const uint32_t *__restrict__ hot, uint32_t *__restrict__ hot_part) {
     partition_tile<KIND, false>(src, num_bins, nb, part, offs, tot, hot, hot_part);

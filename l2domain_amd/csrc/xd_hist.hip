@@ -41,6 +41,11 @@ constexpr uint32_t kBucketBins = 1u << kHB;
 // keys against 208 us at 16384); 24576 measured fastest for the XCD-aware call.
 constexpr int kTileKeys = 24576;
 static_assert(kTileKeys % 4096 == 0 && kTileKeys <= 65536, "tile shape");
+// u16 slots per tile in the workspace: 128 bytes past the tile, so that the runs of tiles 16
+// apart (those one count wave reads together) do not start at the same offset modulo 48 KiB.
+// At 2^28 Zipf keys the count pass took 86.5 us with tiles at kTileKeys, 79.8 / 80.3 / 81.1 us
+// at 64 / 128 / 256 slots more, and 84-86 us at 512 or more.
+constexpr int kPartStride = kTileKeys + 64;
 constexpr int kP1Threads = 1024;
 constexpr int kP1Vec = kTileKeys / 4 / kP1Threads;  // uint4 loads per thread
 constexpr int kMaxBuckets = 512;                    // num_bins <= 2^24
@@ -111,7 +116,7 @@ static HistLayout hist_layout(size_t n, uint32_t num_bins) {
     L.offs = o;
     o = align256(o + (size_t)L.ntiles * (L.nb + 1 + kPeelWords) * sizeof(uint32_t));
     L.part = o;
-    o = align256(o + (size_t)L.ntiles * kTileKeys * sizeof(uint16_t));
+    o = align256(o + (size_t)L.ntiles * kPartStride * sizeof(uint16_t));
     // hot-key table (kHotWords), then one row of kHotSlots counters per tile
     L.hot = o;
     o = align256(o + (size_t)kHotWords * sizeof(uint32_t));
@@ -528,7 +533,7 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
 
     const uint32_t nvec = (tile_total + 7) / 8;  // 8 u16 per 16-byte store
     const uint4 *from = reinterpret_cast<const uint4 *>(stage);
-    uint4 *dst = reinterpret_cast<uint4 *>(part + (size_t)t * kTileKeys);
+    uint4 *dst = reinterpret_cast<uint4 *>(part + (size_t)t * kPartStride);
     for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) dst[i] = from[i];
 }
 
@@ -794,7 +799,7 @@ hist_partition_lean_kernel(PartSrc src, uint32_t bound, int nb, uint16_t *__rest
     }
     const uint32_t nvec = (tile_total + 7) / 8;
     const uint4 *from = reinterpret_cast<const uint4 *>(S.stage);
-    uint4 *dst = reinterpret_cast<uint4 *>(part + (size_t)t * kTileKeys);
+    uint4 *dst = reinterpret_cast<uint4 *>(part + (size_t)t * kPartStride);
     for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) dst[i] = from[i];
 }
 
@@ -1011,7 +1016,7 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
                 ee = in ? rej : ee;
             }
             const uint32_t v = (ss >> 3) + (gc - ex);
-            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + jj * kP2Waves) * kTileKeys);
+            const uint4 *run = reinterpret_cast<const uint4 *>(part + (size_t)(tb + jj * kP2Waves) * kPartStride);
             q = load_stream(&run[v]);  // read once
             e8 = g < T ? 8 * v : ee;
             s0 = ss;

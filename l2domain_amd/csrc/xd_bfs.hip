@@ -41,6 +41,10 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
+#include <memory>
+#include <mutex>
+#include <vector>
 
 #include "xd_common.hpp"
 
@@ -581,6 +585,70 @@ static int build_route(const int32_t *rowptr, const int32_t *col, int32_t V, int
 
 using namespace xd;
 
+namespace {
+
+// Host side of the per-batch control copy: a pinned copy of the control block (a copy into
+// pageable memory is staged by the runtime and cost ~15 us a search) and an event to wait
+// on. Entries are shared by all host threads through one process-wide pool: a call takes an
+// entry of its device (or makes one) and gives it back when it returns, so the pool never
+// holds more entries per device than calls have run at once on it.
+struct CtlHost {
+    int device = -1;
+    BfsCtlBlock *pinned = nullptr;          // hipHostMalloc'd, or null when that failed
+    std::unique_ptr<BfsCtlBlock> pageable;  // fallback copy target
+    hipEvent_t done = nullptr;
+    BfsCtlBlock &block() { return pinned ? *pinned : *pageable; }
+};
+
+std::mutex g_ctl_mu;
+std::vector<CtlHost *> g_ctl_free;
+
+CtlHost *ctl_take(int device) {
+    {
+        std::lock_guard<std::mutex> g(g_ctl_mu);
+        for (size_t i = 0; i < g_ctl_free.size(); ++i)
+            if (g_ctl_free[i]->device == device) {
+                CtlHost *c = g_ctl_free[i];
+                g_ctl_free.erase(g_ctl_free.begin() + (long)i);
+                return c;
+            }
+    }
+    CtlHost *c = new CtlHost;
+    c->device = device;
+    if (hipHostMalloc(reinterpret_cast<void **>(&c->pinned), sizeof(BfsCtlBlock), hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        c->pinned = nullptr;
+        c->pageable.reset(new BfsCtlBlock);
+    }
+    return c;
+}
+
+void ctl_give(CtlHost *c) {
+    std::lock_guard<std::mutex> g(g_ctl_mu);
+    g_ctl_free.push_back(c);
+}
+
+struct CtlLease {
+    CtlHost *c;
+    explicit CtlLease(int device) : c(ctl_take(device)) {}
+    ~CtlLease() { ctl_give(c); }
+};
+
+// Waits for `ev` (made with hipEventBlockingSync): polls for up to 200 us (a level batch
+// usually lands within that, and a blocking wait woke the host later: R-MAT scale 22 ran at
+// 466 instead of 477 GTEPS), then blocks in hipEventSynchronize so that a long batch does not
+// hold a host core.
+hipError_t wait_event(hipEvent_t ev) {
+    const auto t0 = std::chrono::steady_clock::now();
+    hipError_t q;
+    while ((q = hipEventQuery(ev)) == hipErrorNotReady) {
+        if (std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(200)) return hipEventSynchronize(ev);
+    }
+    return q;
+}
+
+}  // namespace
+
 extern "C" {
 
 size_t xd_bfs_workspace_size(int32_t num_vertices, int64_t nnz) {
@@ -635,20 +703,12 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     const auto *blist =
         rt ? reinterpret_cast<const int32_t *>(static_cast<const char *>(rt) + kRouteHeader) : nullptr;
     BfsCtl h{};
-    // The host copy of the control block (25 KiB) lives in pinned memory, allocated once per
-    // thread: a copy into pageable memory is staged by the runtime and cost ~15 us a search.
-    static thread_local BfsCtlBlock *hb_pinned = nullptr;
-    static thread_local BfsCtlBlock hb_pageable;
-    static thread_local bool hb_tried = false;
-    if (!hb_tried) {
-        hb_tried = true;
-        if (hipHostMalloc(reinterpret_cast<void **>(&hb_pinned), sizeof(BfsCtlBlock), hipHostMallocDefault) !=
-            hipSuccess) {
-            (void)hipGetLastError();
-            hb_pinned = nullptr;
-        }
-    }
-    BfsCtlBlock &hb = hb_pinned ? *hb_pinned : hb_pageable;
+    int device = 0;
+    XD_HIP(hipGetDevice(&device));
+    CtlLease lease(device);
+    if (lease.c->done == nullptr)  // (blocking sync: the wait past its polling window sleeps)
+        XD_HIP(hipEventCreateWithFlags(&lease.c->done, hipEventDisableTiming | hipEventBlockingSync));
+    BfsCtlBlock &hb = lease.c->block();
     for (int64_t enq = 0;;) {
         const int batch = enq == 0 ? kFirstBatch : kLevelBatch;
         for (int k = 0; k < batch; ++k, ++enq) {
@@ -659,14 +719,8 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
             if (int rc = launch_status("bfs level kernels")) return rc;
         }
         XD_HIP(hipMemcpyAsync(&hb, st.ctl, sizeof(hb), hipMemcpyDeviceToHost, s));
-        // Wait for the copy by polling an event (one per thread, created once): a blocking
-        // stream synchronize woke the host later (R-MAT scale 22: 466 -> 477 GTEPS).
-        static thread_local hipEvent_t done_ev = nullptr;
-        if (!done_ev) XD_HIP(hipEventCreateWithFlags(&done_ev, hipEventDisableTiming));
-        XD_HIP(hipEventRecord(done_ev, s));
-        hipError_t q;
-        while ((q = hipEventQuery(done_ev)) == hipErrorNotReady) {
-        }
+        XD_HIP(hipEventRecord(lease.c->done, s));
+        const hipError_t q = wait_event(lease.c->done);
         if (q != hipSuccess) return hip_fail(q, "xd_bfs_csr: waiting for the control copy");
         // S_{lv-1} was published by the last level kernel; the step adds that level's totals
         const int lv = (int)enq;

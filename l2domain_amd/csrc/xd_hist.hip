@@ -77,9 +77,11 @@ constexpr int kHotTable = 16384;             // sampling pass: open-addressed LD
 constexpr uint32_t kHotMin = 2;
 constexpr size_t kHotMinKeys = size_t(1) << 20;  // smaller calls skip the sampling launch
 // hot region of the workspace: tab[kHotSlots] (key or kNoKey), perm[kHotSlots] (row position
-// of each slot), sorted[kHotSlots] (key at each row position), first[kMaxBuckets + 1]
-constexpr int kHotTab = 0, kHotPerm = kHotSlots, kHotSorted = 2 * kHotSlots, kHotFirst = 3 * kHotSlots;
-constexpr int kHotWords = 3 * kHotSlots + kMaxBuckets + 1;
+// of each slot), sorted[kHotSlots] (key at each row position), total[kHotSlots] (the count of
+// the key at each row position, summed by the count pass), first[kMaxBuckets + 1]
+constexpr int kHotTab = 0, kHotPerm = kHotSlots, kHotSorted = 2 * kHotSlots, kHotTotal = 3 * kHotSlots,
+              kHotFirst = 4 * kHotSlots;
+constexpr int kHotWords = 4 * kHotSlots + kMaxBuckets + 1;
 
 struct HistBucket {
     int first;  // first item (= partial slot) of this bucket
@@ -247,6 +249,7 @@ __global__ void __launch_bounds__(1024) hist_hot_kernel(const uint32_t *__restri
         hot[kHotTab + tid] = key;
         hot[kHotPerm + tid] = pos;
         hot[kHotSorted + pos] = key;
+        hot[kHotTotal + tid] = 0u;
         ssorted[pos] = key;
         if (tid == 0) s_valid = nvalid;
     }
@@ -835,16 +838,12 @@ struct Deal {
 // slot nzpre + floor(pre * R / N), R = slots beyond one per non-empty bucket, and the slots
 // end exactly at nitems (the clamps only guard the table).
 template <int THREADS>
-__device__ Deal deal_items(const uint32_t *__restrict__ tot, int nb, int nitems, uint32_t *wsum,
-                           const uint32_t *__restrict__ hot_first) {
+__device__ Deal deal_items(const uint32_t *__restrict__ tot, int nb, int nitems, uint32_t *wsum) {
     __shared__ uint32_t s_total, s_nnz;
     const int b = (int)threadIdx.x;
     uint32_t T = 0;
-    if (b < nb) {
+    if (b < nb)
         for (int x = 0; x < kNumXcd; ++x) T += tot[(size_t)x * nb + b];
-        // a bucket with hot-table keys needs a counting item even if all its keys were hot
-        if (hot_first != nullptr && hot_first[b + 1] > hot_first[b]) T += 1;
-    }
     const uint32_t nz = (b < nb && T > 0) ? 1u : 0u;
     const uint32_t pre = block_excl_scan<THREADS>(T, wsum, &s_total);
     const uint32_t N = s_total;
@@ -899,11 +898,12 @@ __device__ __forceinline__ void count_vec(uint32_t *h, const uint4 &q, uint32_t 
 __global__ void __launch_bounds__(kP2Threads)
 hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb, int ntiles,
                   const uint32_t *__restrict__ tot, int per_xcd, uint32_t *__restrict__ partials,
-                  HistBucket *__restrict__ buckets, int mode, unsigned rot, const uint32_t *__restrict__ hot_tab,
+                  HistBucket *__restrict__ buckets, int mode, unsigned rot, uint32_t *__restrict__ hot_tab,
                   const uint32_t *__restrict__ hot_part) {
     __shared__ __attribute__((aligned(16))) uint32_t h[kCountSlots];
     __shared__ uint32_t wsum[kP2Waves];
     __shared__ int s_item[3];  // bucket (-1: idle slot), t0, t1
+    __shared__ uint32_t s_hot[kP2Threads];
     const int g = (int)blockIdx.x;
     const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     int slot;
@@ -915,8 +915,7 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     }
     if (tid == 0) s_item[0] = -1;
     const int nitems = per_xcd * kNumXcd;
-    const uint32_t *hot_first = hot_tab != nullptr ? hot_tab + kHotFirst : nullptr;
-    const Deal d = deal_items<kP2Threads>(tot, nb, nitems, wsum, hot_first);  // synchronises the block
+    const Deal d = deal_items<kP2Threads>(tot, nb, nitems, wsum);  // synchronises the block
     if (tid < nb && d.count > 0 && (uint32_t)slot >= d.first && (uint32_t)slot < d.first + d.count) {
         const uint32_t j = (uint32_t)slot - d.first;
         s_item[0] = tid;
@@ -926,6 +925,33 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     if (g == 0 && tid < nb) buckets[tid] = HistBucket{(int)d.first, (int)d.count};  // the merge pass's view
     uint4 *h4 = reinterpret_cast<uint4 *>(h);
     for (int i = tid; i < (int)(kCountSlots / 4); i += kP2Threads) h4[i] = make_uint4(0, 0, 0, 0);
+    // The hot-table counters: workgroup g sums the rows of tiles [g ntiles / G, (g + 1) ntiles
+    // / G) (G = the grid, whatever its bucket: four threads per row position, eight loads in
+    // flight each) and adds them to the positions' totals, which the merge adds to the keys'
+    // bins. (Summing each bucket's keys over its items' tile ranges read one or two lines
+    // of every row per item, and took 11.5 us of the 64 a median item ran at 2^28 Zipf keys.)
+    if (hot_tab != nullptr) {
+        const int G = (int)gridDim.x;
+        const int ta = (int)((long long)g * ntiles / G), tz = (int)((long long)(g + 1) * ntiles / G);
+        const int pos = tid % kHotSlots, q = tid / kHotSlots;
+        constexpr int Q = kP2Threads / kHotSlots, U = 8;
+        uint32_t acc = 0;
+        for (int tt = ta + q; tt < tz; tt += U * Q) {
+            uint32_t v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = hot_part[(size_t)min(tt + u * Q, tz - 1) * kHotSlots + pos];
+#pragma unroll
+            for (int u = 0; u < U; ++u) acc += tt + u * Q < tz ? v[u] : 0u;
+        }
+        s_hot[tid] = acc;
+        __syncthreads();
+        if (tid < kHotSlots) {
+            uint32_t sum = 0;
+#pragma unroll
+            for (int k = 0; k < Q; ++k) sum += s_hot[k * kHotSlots + tid];
+            if (sum) atomicAdd(hot_tab + kHotTotal + tid, sum);
+        }
+    }
     __syncthreads();
     const int b = s_item[0];
     if (b < 0) return;  // an idle slot (uniform over the block)
@@ -940,28 +966,6 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
         const uint32_t *pw = offs + (size_t)tt * (nb + 1 + kPeelWords) + nb + 1;
         const uint32_t k1 = pw[0], n1 = pw[1];
         if (k1 != kNoKey && (int)(k1 >> kHB) == b && n1) atomicAdd(&h[k1 & (kBucketBins - 1)], n1);
-    }
-    // The hot-table keys of this bucket (ranks [lo, lo + m)): a group of P threads per key sums
-    // its counters over the item's tiles, eight loads in flight per thread.
-    if (hot_tab != nullptr) {
-        const int lo = (int)hot_first[b], m = (int)hot_first[b + 1] - lo;
-        if (m > 0) {
-            const int P = kP2Threads / m;  // m <= kHotSlots: at least 4 threads per key
-            const int j = tid / P, r = tid % P;
-            if (j < m) {
-                const uint32_t *col = hot_part + lo + j;
-                uint32_t acc = 0;
-                constexpr int U = 8;
-                for (int tt = it.t0 + r; tt < it.t1; tt += U * P) {
-                    uint32_t v[U];
-#pragma unroll
-                    for (int u = 0; u < U; ++u) v[u] = col[(size_t)min(tt + u * P, it.t1 - 1) * kHotSlots];
-#pragma unroll
-                    for (int u = 0; u < U; ++u) acc += tt + u * P < it.t1 ? v[u] : 0u;
-                }
-                if (acc) atomicAdd(&h[hot_tab[kHotSorted + lo + j] & (kBucketBins - 1)], acc);
-            }
-        }
     }
     uint32_t hot = kTrash + 1, hot2 = kTrash + 2;  // no hot keys yet (never equal, never a key)
     uint32_t hc = 0, hc2 = 0;
@@ -1093,7 +1097,8 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
 // 4. merge
 // ---------------------------------------------------------------------------------------
 __device__ void merge_unit(int u, const uint32_t *__restrict__ partials, const HistBucket *__restrict__ buckets,
-                           uint32_t num_bins, uint32_t *__restrict__ counts, bool counts16) {
+                           uint32_t num_bins, uint32_t *__restrict__ counts, bool counts16,
+                           const uint32_t *__restrict__ hot) {
     const int b = u / kMergeUnitsPerBucket;
     const int blk = u % kMergeUnitsPerBucket;
     const HistBucket bk = buckets[b];
@@ -1112,6 +1117,21 @@ __device__ void merge_unit(int u, const uint32_t *__restrict__ partials, const H
             acc.w += p.w;
         }
         const uint32_t k = bin0 + 4u * (uint32_t)v;
+        if (hot != nullptr) {
+            // the hot-table keys among bins [k, k + 4): the bucket's keys are sorted ascending
+            const uint32_t lo = hot[kHotFirst + b], hi = hot[kHotFirst + b + 1];
+            for (uint32_t j = lo; j < hi; ++j) {
+                const uint32_t key = hot[kHotSorted + j];
+                if (key >= k + 4) break;
+                if (key >= k) {
+                    const uint32_t c = hot[kHotTotal + j];
+                    acc.x += key == k ? c : 0u;
+                    acc.y += key == k + 1 ? c : 0u;
+                    acc.z += key == k + 2 ? c : 0u;
+                    acc.w += key == k + 3 ? c : 0u;
+                }
+            }
+        }
         if (counts16 && k + 3 < num_bins) {
             reinterpret_cast<uint4 *>(counts + k)[0] = acc;
         } else {
@@ -1125,7 +1145,8 @@ __device__ void merge_unit(int u, const uint32_t *__restrict__ partials, const H
 
 __global__ void __launch_bounds__(kMergeThreads)
 hist_merge_kernel(const uint32_t *__restrict__ partials, const HistBucket *__restrict__ buckets, int nb,
-                  uint32_t num_bins, uint32_t *__restrict__ counts, bool counts16, uint32_t *__restrict__ tot) {
+                  uint32_t num_bins, uint32_t *__restrict__ counts, bool counts16, uint32_t *__restrict__ tot,
+                  const uint32_t *__restrict__ hot) {
     const int g = (int)blockIdx.x;
     if (g == 0)
         for (int i = (int)threadIdx.x; i < kNumXcd * nb; i += kMergeThreads) tot[i] = 0;
@@ -1133,7 +1154,7 @@ hist_merge_kernel(const uint32_t *__restrict__ partials, const HistBucket *__res
     // (its partials in that XCD's L2) measured slower (aware 11.1-11.7 us against 9.5 us),
     // since an XCD whose range is one hot bucket has few units for its 128 workgroups.
     for (int u = g; u < nb * kMergeUnitsPerBucket; u += (int)gridDim.x)
-        merge_unit(u, partials, buckets, num_bins, counts, counts16);
+        merge_unit(u, partials, buckets, num_bins, counts, counts16, hot);
 }
 
 }  // namespace xd
@@ -1260,7 +1281,7 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     // one workgroup per merge unit, up to 4096
     const int merge_grid = std::min(std::max(L.nb * kMergeUnitsPerBucket, kNumXcd * 64), 4096);
     launch("hist_merge_kernel", hist_merge_kernel, dim3(merge_grid), dim3(kMergeThreads), 0, s, partials, buckets, L.nb,
-           num_bins, counts, aligned16(counts), tot);
+           num_bins, counts, aligned16(counts), tot, (const uint32_t *)hot);
     return launch_status("hist_merge_kernel");
 }
 

@@ -5,10 +5,16 @@
 //   subgroup_reduce (141-147): shuffle tree over the 32 lanes of a row
 //   gemv_partitioned_kernel (163-197) / gemv_baseline_kernel (199-231): row placement
 //
-// MI355X design: one wave64 per row at a time, 16-byte (dwordx4) loads of A, x staged once
-// per workgroup in LDS, DPP wave reduction, and a workgroup -> row-chunk map that gives
-// every XCD one contiguous 1/8 of the rows (aware) or interleaves chunks across XCDs
-// (oblivious). No MFMA: GEMV is 0.5 (fp32) or 1 (fp16) flop per byte of A.
+// MI355X design: one wave64 per row at a time, 16-byte (dwordx4) loads of A, DPP wave
+// reduction, and a workgroup -> row-chunk map that gives every XCD one contiguous 1/8 of the
+// rows (aware) or interleaves chunks across XCDs (oblivious). x is read from global memory
+// (L2-resident after the first workgroups) into registers beside the first matrix loads:
+// each lane of the exact, row-home and segment-home kernels needs the same few x vectors for
+// every row or segment it reduces, so staging x in LDS only put a barrier and a round trip
+// ahead of the stream (cold, at 14336 x 4096 fp16: 22.5 -> 21.5 us oblivious, 21.0 -> 20.4 us
+// row-home; 4096^2 fp32 segment-home 14.1 -> 13.5 us). The chunk-home and generic kernels,
+// whose lanes need x at offsets that change from chunk to chunk, keep x in LDS. No MFMA: GEMV
+// is 0.5 (fp32) or 1 (fp16) flop per byte of A.
 #include <hip/hip_runtime.h>
 
 #include <stdlib.h>
@@ -88,8 +94,8 @@ gemv_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__r
 
 // Exact-width variant: each row is split into S segments of 64*CW vectors, one wave per
 // segment, so every lane owns exactly CW vectors and no load needs a bounds check. The
-// first row's loads are issued before x is staged in LDS, so the x round trip overlaps the
-// A stream; with DB the wave's next row is loaded while the current one is reduced.
+// first row's loads are issued before the lane's CW x vectors, which stay in registers for
+// every row; with DB the wave's next row is loaded while the current one is reduced.
 // Partial sums of a split row meet in LDS.
 template <bool F16, int CW, int S, bool DB>
 __global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4)))
@@ -97,7 +103,6 @@ gemv_exact_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, floa
                   int rows_per_wg, int nchunks, int mode, unsigned rot) {
     constexpr int nv = kWave * CW * S;
     constexpr int kRowsPerPass = kGemvWaves / S;
-    extern __shared__ uint4 xs[];
     __shared__ float part[kGemvWaves];
     const int b = (int)blockIdx.x;
     int chunk;
@@ -123,8 +128,9 @@ gemv_exact_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, floa
 #pragma unroll
         for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
     }
-    for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
-    __syncthreads();
+    uint4 xr[CW];
+#pragma unroll
+    for (int u = 0; u < CW; ++u) xr[u] = x[voff + u * kWave];
 
     // Every wave runs the same number of passes so that the LDS combine barrier is uniform.
     for (int base = r0; base < r1; base += kRowsPerPass) {
@@ -141,10 +147,10 @@ gemv_exact_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, floa
         if (live) {
 #pragma unroll
             for (int u = 0; u < CW; u += 2) {
-                const uint4 xv0 = xs[voff + u * kWave];
+                const uint4 xv0 = xr[u];
                 acc0 = F16 ? dot16_f16(a[u], xv0, acc0) : dot16_f32(a[u], xv0, acc0);
                 if (u + 1 < CW) {
-                    const uint4 xv1 = xs[voff + (u + 1) * kWave];
+                    const uint4 xv1 = xr[u + 1];
                     acc1 = F16 ? dot16_f16(a[u + 1], xv1, acc1) : dot16_f32(a[u + 1], xv1, acc1);
                 }
             }
@@ -187,7 +193,6 @@ gemv_rowhome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, fl
                     int mode, HomeMap home) {
     constexpr int nv = kWave * CW;
     constexpr int kGroup = 8;
-    extern __shared__ uint4 xs[];
     const int b = (int)blockIdx.x;
     const int per_die = (int)gridDim.x / 2;
     const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
@@ -195,8 +200,9 @@ gemv_rowhome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, fl
     const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
     const int wave = (int)threadIdx.x / kWave;
     const int lane = (int)threadIdx.x % kWave;
-    for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
-    __syncthreads();
+    uint4 xr[CW];  // the lane's x vectors, the same for every row
+#pragma unroll
+    for (int u = 0; u < CW; ++u) xr[u] = x[u * kWave + lane];
     const uint64_t abase = reinterpret_cast<uint64_t>(A);
     const int ngroups = (M + kGroup - 1) / kGroup;
     for (int g = rank; g < ngroups; g += per_die) {
@@ -214,10 +220,9 @@ gemv_rowhome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, fl
             float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
             for (int u = 0; u < CW; u += 2) {
-                acc0 = F16 ? dot16_f16(a[u], xs[u * kWave + lane], acc0) : dot16_f32(a[u], xs[u * kWave + lane], acc0);
+                acc0 = F16 ? dot16_f16(a[u], xr[u], acc0) : dot16_f32(a[u], xr[u], acc0);
                 if (u + 1 < CW)
-                    acc1 = F16 ? dot16_f16(a[u + 1], xs[(u + 1) * kWave + lane], acc1)
-                               : dot16_f32(a[u + 1], xs[(u + 1) * kWave + lane], acc1);
+                    acc1 = F16 ? dot16_f16(a[u + 1], xr[u + 1], acc1) : dot16_f32(a[u + 1], xr[u + 1], acc1);
             }
             const float acc = wave_sum_f32(acc0 + acc1);
             if (lane == 0) y[row] = acc;
@@ -283,7 +288,6 @@ gemv_seghome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, fl
     constexpr int CW = 8;
     constexpr int kSegVec = kWave * CW;  // 512 vectors = 8 KiB
     constexpr int kGroup = 8;
-    extern __shared__ uint4 xs[];
     const int b = (int)blockIdx.x;
     const int per_die = (int)gridDim.x / 2;
     const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
@@ -291,103 +295,42 @@ gemv_seghome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, fl
     const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
     const int wave = (int)threadIdx.x / kWave;
     const int lane = (int)threadIdx.x % kWave;
-    const int nv = S * kSegVec;
-    // x is staged after the first A loads are issued (before them it put a round trip ahead
-    // of the stream, which a cold call pays in full)
-    auto stage_x = [&] {
-        for (int i = (int)threadIdx.x; i < nv; i += kGemvThreads) xs[i] = x[i];
-        __syncthreads();
-    };
     const uint64_t abase = reinterpret_cast<uint64_t>(A);
     const int nseg = M * S;
     const int ngroups = (nseg + kGroup - 1) / kGroup;
-    // one segment j: loaded, reduced, met (the general path)
-    auto one_segment = [&](int j) {
-        const int row = j / S;
-        const int seg = j - row * S;
-        const uint4 *p = A + (size_t)j * kSegVec + lane;
-        uint4 a[CW];
-#pragma unroll
-        for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
-        const uint4 *xv = xs + seg * kSegVec + lane;
-        float acc0 = 0.0f, acc1 = 0.0f;
-#pragma unroll
-        for (int u = 0; u < CW; u += 2) {
-            acc0 = F16 ? dot16_f16(a[u], xv[u * kWave], acc0) : dot16_f32(a[u], xv[u * kWave], acc0);
-            acc1 = F16 ? dot16_f16(a[u + 1], xv[(u + 1) * kWave], acc1) : dot16_f32(a[u + 1], xv[(u + 1) * kWave], acc1);
-        }
-        const float part = wave_sum_f32(acc0 + acc1);
-        if (lane == 0) seg_meet<F16, PAIR>(part, j, row, seg, S, y, cnt, slot);
-    };
-    if (PAIR) {
-        // Rows of two segments: a group of 8 segments holds 4 rows, each with one segment on
-        // either die when the home function splits every 16 KiB pair (page map, or a mask with
-        // bit 13), so each of the 4 waves takes one wanted segment of a group. A wave takes its
-        // segments of two groups at once: both segments' loads in flight, both reduced, then
-        // both exchanges in one instruction (lanes 0 and 1). An exchange after every segment
-        // (the returning atomic waits for every load issued before it) held the second
-        // segment's loads back by a memory round trip. A wave's second segment of a group
-        // (other home functions) takes the general path.
-        const uint4 *xv = xs + lane;
-        bool staged = false;
-        for (int g0 = rank; g0 < ngroups || !staged; g0 += 2 * per_die) {
-            int jj[2], extra[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int g = g0 + t * per_die;
-                const int jl = g * kGroup + lane;
-                const bool wanted = g < ngroups && lane < kGroup && jl < nseg &&
-                                    home(abase + (uint64_t)jl * kHomeChunk) == want;
-                uint64_t m = __ballot(wanted);
-                for (int k = 0; k < wave && m; ++k) m &= m - 1;
-                jj[t] = m ? g * kGroup + __builtin_ctzll(m) : -1;  // (wave-uniform)
-                for (int k = 0; k < kGemvWaves && m; ++k) m &= m - 1;
-                extra[t] = m ? g * kGroup + __builtin_ctzll(m) : -1;  // at most one more: 8 per group
-            }
-            uint4 a[2][CW];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const uint4 *p = A + (size_t)(jj[t] >= 0 ? jj[t] : 0) * kSegVec + lane;  // (clamped: no load under a branch)
-#pragma unroll
-                for (int u = 0; u < CW; ++u) a[t][u] = p[u * kWave];
-            }
-            if (!staged) {  // (uniform over the workgroup: the first pass of every wave)
-                stage_x();
-                staged = true;
-                if (g0 >= ngroups) break;  // a workgroup with no groups only joined the barrier
-            }
-            float part[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const uint4 *xt = xv + (jj[t] >= 0 ? jj[t] % S : 0) * kSegVec;
-                float acc0 = 0.0f, acc1 = 0.0f;
-#pragma unroll
-                for (int u = 0; u < CW; u += 2) {
-                    acc0 = F16 ? dot16_f16(a[t][u], xt[u * kWave], acc0) : dot16_f32(a[t][u], xt[u * kWave], acc0);
-                    acc1 = F16 ? dot16_f16(a[t][u + 1], xt[(u + 1) * kWave], acc1)
-                               : dot16_f32(a[t][u + 1], xt[(u + 1) * kWave], acc1);
-                }
-                part[t] = wave_sum_f32(acc0 + acc1);
-            }
-            // lane t meets segment jj[t]: the exact kernel's bits (p0 + p1, in segment order)
-            const int jm = lane == 0 ? jj[0] : jj[1];
-            if (lane < 2 && jm >= 0) {
-                const float pm = lane == 0 ? part[0] : part[1];
-                const int row = jm / S, seg = jm - row * S;
-                seg_meet<F16, true>(pm, jm, row, seg, S, y, cnt, slot);
-            }
-#pragma unroll
-            for (int t = 0; t < 2; ++t)
-                if (extra[t] >= 0) one_segment(extra[t]);  // (wave-uniform)
-        }
-        return;
-    }
-    stage_x();
-    for (int g = rank; g < ngroups; g += per_die) {
+    // the wanted segments of group g, minus the first `wave` of them (every 4th is this wave's)
+    auto wanted_of = [&](int g) -> uint64_t {
         const int jl = g * kGroup + lane;
         const bool wanted = lane < kGroup && jl < nseg && home(abase + (uint64_t)jl * kHomeChunk) == want;
         uint64_t m = __ballot(wanted);
         for (int k = 0; k < wave && m; ++k) m &= m - 1;
+        return m;
+    };
+    // segment j: its matrix vectors and the matching x vectors (segment j % S of x) loaded
+    // together, then reduced and met. (x staged in LDS instead: 14.1 against 13.5 us cold at
+    // 4096 x 4096 fp32; two groups' segments taken at once, both exchanges in one
+    // instruction: 0.25 us faster cold, 1.6 us slower warm.)
+    auto one_segment = [&](int j) {
+        const int row = j / S;
+        const int seg = j - row * S;
+        uint4 a[CW], xv[CW];
+        const uint4 *p = A + (size_t)j * kSegVec + lane;
+        const uint4 *xp = x + (size_t)seg * kSegVec + lane;
+#pragma unroll
+        for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
+#pragma unroll
+        for (int u = 0; u < CW; ++u) xv[u] = xp[u * kWave];
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int u = 0; u < CW; u += 2) {
+            acc0 = F16 ? dot16_f16(a[u], xv[u], acc0) : dot16_f32(a[u], xv[u], acc0);
+            acc1 = F16 ? dot16_f16(a[u + 1], xv[u + 1], acc1) : dot16_f32(a[u + 1], xv[u + 1], acc1);
+        }
+        const float part = wave_sum_f32(acc0 + acc1);
+        if (lane == 0) seg_meet<F16, PAIR>(part, j, row, seg, S, y, cnt, slot);
+    };
+    for (int g = rank; g < ngroups; g += per_die) {
+        uint64_t m = wanted_of(g);
         while (m) {
             one_segment(g * kGroup + __builtin_ctzll(m));
             for (int k = 0; k < kGemvWaves && m; ++k) m &= m - 1;
@@ -573,10 +516,10 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         sgrid = (sgrid + kNumXcd - 1) / kNumXcd * kNumXcd;
         if (sgrid > (1LL << 30)) return fail(XD_ERR_UNSUPPORTED, "gemv: matrix too large for the split-row route");
         if (S == 2)
-            launch("gemv_seghome_kernel", gemv_seghome_kernel<F16, true>, dim3((unsigned)sgrid), dim3(kGemvThreads), lds, s, A4, x4,
+            launch("gemv_seghome_kernel", gemv_seghome_kernel<F16, true>, dim3((unsigned)sgrid), dim3(kGemvThreads), 0, s, A4, x4,
                                y, M, S, mode, home, cnt, slot);
         else
-            launch("gemv_seghome_kernel", gemv_seghome_kernel<F16, false>, dim3((unsigned)sgrid), dim3(kGemvThreads), lds, s, A4,
+            launch("gemv_seghome_kernel", gemv_seghome_kernel<F16, false>, dim3((unsigned)sgrid), dim3(kGemvThreads), 0, s, A4,
                                x4, y, M, S, mode, home, cnt, slot);
         done = true;
     }
@@ -615,7 +558,7 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         done = true;
 #define XD_GEMV_HOME(CC)                                                                                       \
     if (CW == CC) {                                                                                           \
-        launch("gemv_rowhome_kernel", gemv_rowhome_kernel<F16, CC>, dim3(hgrid), dim3(kGemvThreads), lds, s, A4, x4, y, M, \
+        launch("gemv_rowhome_kernel", gemv_rowhome_kernel<F16, CC>, dim3(hgrid), dim3(kGemvThreads), 0, s, A4, x4, y, M, \
                            mode, home);                                                                        \
     } else
         XD_GEMV_HOME(1)
@@ -634,7 +577,7 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         done = true;
 #define XD_GEMV_EXACT(CC, SS, DBB)                                                                        \
     if (CW == CC && S == SS) {                                                                          \
-        launch("gemv_exact_kernel", gemv_exact_kernel<F16, CC, SS, DBB>, dim3(grid), dim3(kGemvThreads), lds, s, A4, \
+        launch("gemv_exact_kernel", gemv_exact_kernel<F16, CC, SS, DBB>, dim3(grid), dim3(kGemvThreads), 0, s, A4, \
                            x4, y, M, rpw, nchunks, mode, rot);                                          \
     } else
         XD_GEMV_EXACT(1, 1, true)

@@ -134,3 +134,36 @@ def test_route_and_per_call_lists_agree():
         _lib.call("xd_bfs_csr", ptr(g.rowptr), ptr(g.col), g.V, g.nnz, 5, ptr(g.level), mode_id(mode), None,
                   ptr(g.workspace), g.workspace.numel(), stream_handle(), C.byref(st))
         np.testing.assert_array_equal(g.level.cpu().numpy().view(np.uint32), ref)
+
+
+def test_concurrent_host_threads():
+    """Two host threads search two graphs at once, each on its own stream: the host side's
+    pinned control copies and events come from one process-wide pool, one entry per call in
+    flight, and every search still matches the oracle."""
+    import threading
+
+    import torch
+    graphs = [ora.rmat_csr(13, 8, 11), ora.rmat_csr(12, 16, 12)]
+    refs = [ora.bfs(r, c, 5)[0] for r, c in graphs]
+    gs = [Graph(r, c) for r, c in graphs]
+    errors = []
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream()
+            for k in range(6):
+                level, _ = gs[i].bfs(5, mode=MODES[k % 3], stream=s)
+                s.synchronize()
+                got = level.cpu().numpy().view(np.uint32)
+                if not np.array_equal(got, refs[i]):
+                    errors.append((i, k))
+        except Exception as e:  # reported below
+            errors.append((i, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+    assert not any(t.is_alive() for t in threads)
+    assert not errors, errors

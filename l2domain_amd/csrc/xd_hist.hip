@@ -331,10 +331,10 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
     const int lane = tid % kWave;
     const int wave = tid / kWave;
     int S = kWave;
-    while (S > 1 && nb * S > kColCounters) S >>= 1;
+    while (S > 1 && nb * S > (int)kColCounters) S >>= 1;
     const int ncol = nb * S;
     const uint32_t my_col = (uint32_t)(lane & (S - 1));
-    for (int i = tid; i < kColCounters + kWave; i += kP1Threads) col[i] = 0;
+    for (int i = tid; i < (int)kColCounters + kWave; i += kP1Threads) col[i] = 0;
 
     // Full / routed: tiles of 16-byte vectors; a vector past the end of the range is loaded
     // clamped to the last one and its keys become spares, so no load sits under a branch

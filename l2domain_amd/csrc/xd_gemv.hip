@@ -17,7 +17,6 @@
 // is 0.5 (fp32) or 1 (fp16) flop per byte of A.
 #include <hip/hip_runtime.h>
 
-#include <stdlib.h>
 
 #include <algorithm>
 
@@ -469,11 +468,6 @@ static int seg_per_row(int K, int elem_bytes) {
 }
 
 static int rows_per_workgroup(int M, int nv) {
-    // XD_GEMV_ROWS_PER_WG overrides the heuristic (tuning sweeps); must be a multiple of 4.
-    if (const char *e = getenv("XD_GEMV_ROWS_PER_WG")) {
-        int v = atoi(e);
-        if (v >= kGemvWaves && v % kGemvWaves == 0) return v;
-    }
     // Aim for >= 4 workgroups per CU on 256 CUs and one row per wave for long rows.
     int rpw = kGemvWaves;
     while ((long long)M / (rpw * 2) >= 1024 && nv * 16 * rpw * 2 <= 256 * 1024) rpw *= 2;
@@ -532,11 +526,9 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         float *part = reinterpret_cast<float *>(workspace);
         // about four pairs (one chunk each) per wave: at 4096 x 14336 fp16 the chunk kernel
         // took 19.8 / 16.3 / 15.6 / 15.9 us warm and 26.6 / 23.1 / 23.2 / 24.0 us cold at 1, 2,
-        // 4, 8 pairs (XD_GEMV_CHUNK_PAIRS_PER_WAVE overrides it for tuning sweeps)
+        // 4, 8 pairs
         const long long npairs = (long long)M * Hh / 4 + 2;
-        long long ppw = 4;
-        if (const char *e = getenv("XD_GEMV_CHUNK_PAIRS_PER_WAVE"))
-            if (atoll(e) >= 1) ppw = atoll(e);
+        constexpr long long ppw = 4;
         long long cgrid = (npairs + 4 * ppw - 1) / (4 * ppw) * 2;
         cgrid = std::max<long long>(kNumXcd, (cgrid + kNumXcd - 1) / kNumXcd * kNumXcd);
         if (cgrid > (1LL << 30)) return fail(XD_ERR_UNSUPPORTED, "gemv: matrix too large for the chunk-home route");

@@ -157,8 +157,7 @@ class GemvF32(Workload):
         return ok
 
     def roof_kernels(self, mode):
-        return ("gemv_kernel", "gemv_exact_kernel", "gemv_rowhome_kernel", "gemv_seghome_kernel",
-                "gemv_chunkhome_kernel", "gemv_pieces_kernel")
+        return ("gemv_kernel", "gemv_exact_kernel", "gemv_rowhome_kernel", "gemv_seghome_kernel")
 
     def roof_footprint(self):
         return self.A

@@ -238,10 +238,8 @@ int xd_read_stream(const void *buf, size_t bytes, int mode, const uint8_t *home_
 
 /* Workspace bytes the GEMV entry points use for the split-row home routing of an M x K
  * matrix of elem_bytes (4: fp32, 2: fp16) elements: M * (S + 1) * 4 when a row is S >= 2
- * whole 8 KiB chunks, M * (P + 1) * 4 with P = (H + 1) / 2 when M is even and a row is an
- * odd number H >= 3 of 4 KiB halves (rows <= 64 KiB in both cases), else 0 (no workspace
- * used). No counterpart in the reference (its rows never span two sides' memory,
- * GEMV.cu:264-273). */
+ * whole 8 KiB chunks (rows <= 64 KiB), else 0 (no workspace used). No counterpart in the
+ * reference (its rows never span two sides' memory, GEMV.cu:264-273). */
 size_t xd_gemv_workspace_size(int M, int K, int elem_bytes);
 
 /* fp32 GEMV. Replaces gemv_partitioned_kernel / gemv_baseline_kernel
@@ -253,10 +251,8 @@ size_t xd_gemv_workspace_size(int M, int K, int elem_bytes);
  *   XD_MODE_AWARE      with A 8 KiB aligned, work follows memory homes (home_attr =
  *                      xd_home_map() of A; NULL = the address-mask prediction):
  *                      rows that divide 8 KiB go whole to the I/O die homing them; rows of
- *                      S >= 2 whole 8 KiB chunks, or (M even) of an odd number of 4 KiB
- *                      halves, are split into their 8 KiB chunks (a chunk may end one row
- *                      and start the next), each reduced on its home die and combined in
- *                      chunk order (needs a workspace of
+ *                      S >= 2 whole 8 KiB chunks are split into their chunks, each reduced
+ *                      on its home die and combined in chunk order (needs a workspace of
  *                      xd_gemv_workspace_size() bytes, 8-byte aligned, zero-filled once when
  *                      allocated; each call leaves it zeroed; calls sharing one workspace
  *                      must not overlap).

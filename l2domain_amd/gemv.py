@@ -14,8 +14,8 @@ from ._torch import mode_id, ptr, stream_handle
 
 def workspace(M: int, K: int, dtype: torch.dtype, device="cuda") -> torch.Tensor | None:
     """Zero-filled workspace for the split-row home routing of an M x K matrix, or None when
-    that route does not apply to the shape (rows neither a whole number >= 2 of 8 KiB chunks
-    nor, with M even, an odd number >= 3 of 4 KiB halves). Every gemv call leaves it zeroed,
+    that route does not apply to the shape (rows not a whole number >= 2 of 8 KiB chunks).
+    Every gemv call leaves it zeroed,
     so it is allocated once and reused."""
     elem = torch.empty((), dtype=dtype).element_size()
     n = int(_lib.lib.xd_gemv_workspace_size(M, K, elem))

@@ -239,47 +239,39 @@ gemv_rowhome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, fl
 //   S == 2 (PAIR): each arrival swaps a 64-bit word (segment + 1) << 32 | bits(partial) into
 //     the row's word; the arrival that gets its partner's word back writes y = p0 + p1
 //     (fp addition is commutative, so the order of arrival does not change the bits) and
-//     clears the word. One round trip per segment.
-//   S > 2: each arrival deposits its partial in slot j with a returning swap, then takes a
-//     ticket on the row's counter; the last of the S arrivals swaps the slots back out,
-//     adds them in segment order, writes y and clears the counter.
+//     clears the word (in the kernel below).
+//   S > 2 (seg_meet): each arrival deposits its partial in slot j with a returning swap, then
+//     takes a ticket on the row's counter; the last of the S arrivals swaps the slots back
+//     out, adds them in segment order, writes y and clears the counter.
 // Both orders equal the exact kernel's LDS combine order, so both kernels give the same bits
 // for S = 2 and 4. The row words / counters must be zero when the call starts; every call
 // leaves them zero.
-template <bool F16, bool PAIR>
 __device__ __forceinline__ void seg_meet(float part, int j, int row, int seg, int S, float *__restrict__ y,
                                          uint32_t *__restrict__ cnt, uint32_t *__restrict__ slot) {
-    if (PAIR) {
-        unsigned long long *pair = reinterpret_cast<unsigned long long *>(cnt);
-        const unsigned long long word =
-            ((unsigned long long)(seg + 1) << 32) | (unsigned long long)__float_as_uint(part);
-        const unsigned long long old = atomicExch(&pair[row], word);
-        if (old != 0ull) {
-            y[row] = part + __uint_as_float((uint32_t)old);
-            atomicExch(&pair[row], 0ull);
+    const uint32_t old = atomicExch(&slot[j], __float_as_uint(part));
+    // consuming the returned value makes the ticket wait until the deposit is done
+    asm volatile("" ::"v"(old));
+    const uint32_t t = atomicAdd(&cnt[row], 1u);
+    if (t == (uint32_t)(S - 1)) {
+        float sum = 0.0f;
+        for (int s = 0; s < S; ++s) {
+            // a swap is a read-modify-write executed at the memory-side atomic unit, like
+            // the deposit it reads (an idempotent OR could become a plain load)
+            const float v = (s == seg) ? part : __uint_as_float(atomicExch(&slot[(size_t)row * S + s], 0u));
+            sum = (s == 0) ? v : sum + v;
         }
-    } else {
-        const uint32_t old = atomicExch(&slot[j], __float_as_uint(part));
-        // consuming the returned value makes the ticket wait until the deposit is done
-        asm volatile("" ::"v"(old));
-        const uint32_t t = atomicAdd(&cnt[row], 1u);
-        if (t == (uint32_t)(S - 1)) {
-            float sum = 0.0f;
-            for (int s = 0; s < S; ++s) {
-                // a swap is a read-modify-write executed at the memory-side atomic unit, like
-                // the deposit it reads (an idempotent OR could become a plain load)
-                const float v = (s == seg) ? part : __uint_as_float(atomicExch(&slot[(size_t)row * S + s], 0u));
-                sum = (s == 0) ? v : sum + v;
-            }
-            y[row] = sum;
-            atomicExch(&cnt[row], 0u);
-        }
+        y[row] = sum;
+        atomicExch(&cnt[row], 0u);
     }
 }
 
 // Workgroup w of a die visits groups w, w + W, w + 2W, ... of 8 consecutive segments (W =
-// workgroups per die); lane i of every wave evaluates the home of segment i of the group,
-// and the group's wanted segments are dealt to the 4 waves in turn.
+// workgroups per die); the lanes of every wave evaluate the homes of the next 8 such groups
+// at once (one page-map load per lane), and each group's wanted segments are dealt to the 4
+// waves in turn. S == 2: a segment's exchange is issued after its reduction and its returned
+// word is used only after the wave's next segment's loads are out, so the round trip overlaps
+// them (the vector-memory counter is in order: the swap is older than those loads, and the
+// wait for it leaves them in flight). 4096 x 4096 fp32 cold: 13.67 -> 13.48 us.
 template <bool F16, bool PAIR>
 __global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4)))
 gemv_seghome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__restrict__ y, int M, int S,
@@ -297,44 +289,72 @@ gemv_seghome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, fl
     const uint64_t abase = reinterpret_cast<uint64_t>(A);
     const int nseg = M * S;
     const int ngroups = (nseg + kGroup - 1) / kGroup;
-    // the wanted segments of group g, minus the first `wave` of them (every 4th is this wave's)
-    auto wanted_of = [&](int g) -> uint64_t {
-        const int jl = g * kGroup + lane;
-        const bool wanted = lane < kGroup && jl < nseg && home(abase + (uint64_t)jl * kHomeChunk) == want;
-        uint64_t m = __ballot(wanted);
-        for (int k = 0; k < wave && m; ++k) m &= m - 1;
-        return m;
-    };
     // segment j: its matrix vectors and the matching x vectors (segment j % S of x) loaded
-    // together, then reduced and met. (x staged in LDS instead: 14.1 against 13.5 us cold at
-    // 4096 x 4096 fp32; two groups' segments taken at once, both exchanges in one
-    // instruction: 0.25 us faster cold, 1.6 us slower warm.)
-    auto one_segment = [&](int j) {
-        const int row = j / S;
-        const int seg = j - row * S;
-        uint4 a[CW], xv[CW];
+    // together, then the previous segment's meet settled, then j reduced and its meet issued.
+    auto seg_loads = [&](int j, uint4 (&a)[CW], uint4 (&xv)[CW]) {
+        const int seg = j % S;
         const uint4 *p = A + (size_t)j * kSegVec + lane;
         const uint4 *xp = x + (size_t)seg * kSegVec + lane;
 #pragma unroll
         for (int u = 0; u < CW; ++u) a[u] = p[u * kWave];
 #pragma unroll
         for (int u = 0; u < CW; ++u) xv[u] = xp[u * kWave];
+    };
+    auto seg_sum = [&](const uint4 (&a)[CW], const uint4 (&xv)[CW]) {
         float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
         for (int u = 0; u < CW; u += 2) {
             acc0 = F16 ? dot16_f16(a[u], xv[u], acc0) : dot16_f32(a[u], xv[u], acc0);
             acc1 = F16 ? dot16_f16(a[u + 1], xv[u + 1], acc1) : dot16_f32(a[u + 1], xv[u + 1], acc1);
         }
-        const float part = wave_sum_f32(acc0 + acc1);
-        if (lane == 0) seg_meet<F16, PAIR>(part, j, row, seg, S, y, cnt, slot);
+        return wave_sum_f32(acc0 + acc1);
     };
-    for (int g = rank; g < ngroups; g += per_die) {
-        uint64_t m = wanted_of(g);
-        while (m) {
-            one_segment(g * kGroup + __builtin_ctzll(m));
-            for (int k = 0; k < kGemvWaves && m; ++k) m &= m - 1;
+    unsigned long long *pw = reinterpret_cast<unsigned long long *>(cnt);
+    int prow = -1;
+    float ppart = 0.0f;
+    unsigned long long pold = 0ull;
+    auto settle = [&]() {
+        if (lane == 0 && prow >= 0 && pold != 0ull) {
+            y[prow] = ppart + __uint_as_float((uint32_t)pold);
+            atomicExch(&pw[prow], 0ull);
+        }
+    };
+    // lane l evaluates segment l % 8 of the l / 8-th of the next 8 groups this workgroup visits
+    for (int g0 = rank; g0 < ngroups; g0 += kGroup * per_die) {
+        const int gl = g0 + (lane / kGroup) * per_die;
+        const int jl = gl * kGroup + lane % kGroup;
+        const bool wanted = gl < ngroups && jl < nseg && home(abase + (uint64_t)jl * kHomeChunk) == want;
+        const uint64_t all = __ballot(wanted);
+        for (int q = 0; q < kGroup; ++q) {
+            const int g = g0 + q * per_die;
+            if (g >= ngroups) break;
+            uint64_t m = (all >> (q * kGroup)) & 0xffull;
+            for (int k = 0; k < wave && m; ++k) m &= m - 1;
+            while (m) {
+                const int j = g * kGroup + __builtin_ctzll(m);
+                uint4 a[CW], xv[CW];
+                seg_loads(j, a, xv);
+                if (PAIR) {
+                    settle();
+                    const float part = seg_sum(a, xv);
+                    const int row = j / S;
+                    if (lane == 0) {
+                        const unsigned long long word =
+                            ((unsigned long long)(j - row * S + 1) << 32) | (unsigned long long)__float_as_uint(part);
+                        pold = atomicExch(&pw[row], word);
+                    }
+                    prow = row;
+                    ppart = part;
+                } else {
+                    const float part = seg_sum(a, xv);
+                    const int row = j / S;
+                    if (lane == 0) seg_meet(part, j, row, j - row * S, S, y, cnt, slot);
+                }
+                for (int k = 0; k < kGemvWaves && m; ++k) m &= m - 1;
+            }
         }
     }
+    if (PAIR) settle();
 }
 
 // Rows that straddle 8 KiB chunks without being whole chunks (the fp16 down projection's

@@ -633,6 +633,13 @@ hist_partition_lean_kernel(PartSrc src, uint32_t bound, int nb, uint16_t *__rest
         t = src.tile0 + g;
     }
 
+    // the table words first: the first barrier waits for them, and the counter is in order
+    uint32_t my_perm = 0, my_tab = 0;
+    if (tid < kHotSlots) {
+        my_tab = hot[kHotTab + tid];
+        my_perm = hot[kHotPerm + tid];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t kk[4 * kP1Vec];
     auto put = [&](int j, const uint4 &v) {
         kk[4 * j] = v.x;
@@ -690,13 +697,9 @@ hist_partition_lean_kernel(PartSrc src, uint32_t bound, int nb, uint16_t *__rest
     // counters zeroed and the table copied in after the loads are issued
     for (int i = tid; i < kLeanRows * kWave; i += kP1Threads) S.col[i] = 0;
     for (int i = tid; i < kHotCopies * kLeanCopyStride; i += kP1Threads) S.cnt[i] = 0;
-    uint32_t my_perm = 0;
-    if (tid < kHotSlots) {
-        S.tab[tid] = hot[kHotTab + tid];
-        my_perm = hot[kHotPerm + tid];
-    }
-#pragma unroll
-    for (int j = 0; j < 4 * kP1Vec; ++j) kk[j] = min(kk[j], bound);
+    if (tid < kHotSlots) S.tab[tid] = my_tab;
+    // the counters and the table are in LDS before any wave reads them; the keys are clamped
+    // batch by batch below, so a batch waits only for its own loads
     __syncthreads();
 
     // One returning add per key (byte offsets into S): a hot key's counter copy, else the key's
@@ -712,6 +715,8 @@ hist_partition_lean_kernel(PartSrc src, uint32_t bound, int nb, uint16_t *__rest
 #pragma unroll
     for (int j0 = 0; j0 < 4 * kP1Vec; j0 += kBatch) {
         uint32_t e[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) kk[j0 + j] = min(kk[j0 + j], bound);
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) e[j] = S.tab[hot_slot(kk[j0 + j])];
         // the batch's offsets, then its adds back to back, then the packing (a hot offset is at

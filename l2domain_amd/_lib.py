@@ -73,6 +73,7 @@ SIGNATURES: dict[str, tuple] = {
     "xd_timing_query": (I, [I, C.c_char_p, I, C.POINTER(D), C.POINTER(C.c_longlong)]),
     "xd_topology_query": (I, [I, C.POINTER(Topology)]),
     "xd_domain_scan": (I, [I, VP, VP]),
+    "xd_xcd_offset": (I, [VP]),
     "xd_home_mask": (U64, []),
     "xd_set_home_mask": (I, [U64]),
     "xd_home_map_pages": (SZ, [VP, SZ]),

@@ -414,7 +414,8 @@ __device__ __forceinline__ void bu_blocks(const BfsState &st, int32_t v0a, int32
 // One level in the direction the control block names.
 __global__ void __launch_bounds__(kBfsThreads)
 bfs_level_kernel(BfsState st, int L, int mode, const int32_t *__restrict__ blist,
-                 const unsigned long long *__restrict__ bcount, int64_t nblocks) {
+                 const unsigned long long *__restrict__ bcount, int64_t nblocks, XcdHint xh) {
+    report_xcd(xh);
     bool heavy = false;
     const int dir = level_dir(st, L, &heavy);
     if (dir == kDone) return;
@@ -470,11 +471,11 @@ bfs_level_kernel(BfsState st, int L, int mode, const int32_t *__restrict__ blist
         // quarter instead, so that a vertex range's lines stay in one L2 from level to level,
         // measured slower: the heavy first bottom-up level took 33.6 against 31.3 us.)
         const int b = (int)blockIdx.x;
-        const uint32_t die = wg_die(b);
+        const uint32_t die = wg_die(b, xh);
         const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
         const int32_t *mine = blist + (int64_t)want * nblocks;
         const int64_t cnt = (int64_t)bcount[want];
-        const int64_t rank = (int64_t)(b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
+        const int64_t rank = (int64_t)die_rank(b, xh);
         const int64_t wd = rank * kWavesPerWg + wave;  // wave of the die
         const int64_t xstride = 2 * (int64_t)(gridDim.x / 2) * kWavesPerWg;
         for (int64_t i = 2 * wd; i < cnt; i += xstride) {
@@ -711,10 +712,11 @@ int xd_bfs_csr(const int32_t *rowptr, const int32_t *col, int32_t V, int64_t nnz
     BfsCtlBlock &hb = lease.c->block();
     for (int64_t enq = 0;;) {
         const int batch = enq == 0 ? kFirstBatch : kLevelBatch;
+        const XcdHint xh = xcd_hint(s);
         for (int k = 0; k < batch; ++k, ++enq) {
             const int lv = (int)(enq + 1);
             launch("bfs_level_kernel", bfs_level_kernel, dim3(kBfsGrid), dim3(kBfsThreads), 0, s, st, lv, bmode, blist,
-                   bcount, L.nblocks);
+                   bcount, L.nblocks, xh);
             launch("bfs_hubs_kernel", bfs_hubs_kernel, dim3(kBigGrid), dim3(kBfsThreads), 0, s, st, lv);
             if (int rc = launch_status("bfs level kernels")) return rc;
         }

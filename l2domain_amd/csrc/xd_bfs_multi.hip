@@ -155,8 +155,10 @@ multi_seed_kernel(const int32_t *__restrict__ sources, int32_t nsrc, const uint8
 __global__ void __launch_bounds__(kMThreads)
 multi_level_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict__ col,
                    const uint8_t *__restrict__ work_side, uint32_t *__restrict__ level, unsigned long long *visited,
-                   int32_t *queues, uint32_t *counts, int32_t V, uint32_t depth, int lg, int mode, int cur) {
+                   int32_t *queues, uint32_t *counts, int32_t V, uint32_t depth, int lg, int mode, int cur,
+                   XcdHint xh) {
     __shared__ int32_t sbuf[kMWaves][2 * kMStage];
+    report_xcd(xh);
     const int nxt = (cur + 1) % 3, clr = (cur + 2) % 3;
     const int b = (int)blockIdx.x, grid = (int)gridDim.x;
     if (b == 0 && threadIdx.x < 2 * kMSub) counts[2 * kMSub * clr + threadIdx.x] = 0u;
@@ -167,9 +169,9 @@ multi_level_kernel(const int32_t *__restrict__ rowptr, const int32_t *__restrict
         rank = b;
         nwg = grid;
     } else {
-        rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
+        rank = die_rank(b, xh);
         nwg = grid / 2;
-        side = wg_die(b) ^ (mode == XD_MODE_ROTATED ? 1u : 0u);
+        side = wg_die(b, xh) ^ (mode == XD_MODE_ROTATED ? 1u : 0u);
     }
     // the frontier this workgroup consumes: kMSub sub-queues, prefix sums of their lengths
     const uint32_t *ccnt = counts + (size_t)(2 * cur + side) * kMSub;
@@ -293,9 +295,10 @@ int xd_bfs_multi(const int32_t *rowptr, const int32_t *col, int32_t num_vertices
                            sources, num_sources, work_side, routed, level, visited, queues, counts, V);
         if (int rc = launch_status("multi_seed_kernel")) return rc;
     }
+    const XcdHint xh = xcd_hint(s);
     for (int32_t d = 0; d < max_depth; ++d) {
         launch("multi_level_kernel", multi_level_kernel, dim3(kMGrid), dim3(kMThreads), 0, s, rowptr, col, work_side, level,
-                           visited, queues, counts, V, (uint32_t)d, lg, mode, d % 3);
+                           visited, queues, counts, V, (uint32_t)d, lg, mode, d % 3, xh);
         if (int rc = launch_status("multi_level_kernel")) return rc;
     }
     return XD_OK;

@@ -88,20 +88,41 @@ __device__ __forceinline__ uint32_t hw_id_word() {
     return v;
 }
 
-// Logical placement of workgroup `wg` in a grid whose size is a multiple of 8, under the
-// round-robin workgroup -> XCD dispatch of CDNA3/4 in SPX mode (wg i runs on XCD i mod 8,
-// verified by xd_domain_scan). `slice` is the data slice this workgroup serves.
+// Workgroup -> XCD placement. CDNA3/4 in SPX mode deal a dispatch's workgroups to the 8 XCDs
+// round robin from a starting XCD that belongs to the queue: workgroup i runs on XCD
+// (i + off) mod 8, with off fixed per queue (measured with xd_domain_scan on nine streams:
+// 0 on the queues a process uses first, 5, 6 or 7 on queues mapped later, the same for every
+// dispatch of a queue). A launcher passes the offset the last aware dispatch on its stream
+// reported (XcdHint, 0 before the first), so placement is right from a stream's second call
+// on; every data assignment stays a function of blockIdx alone, so a stale offset only
+// misplaces work, never changes a result.
+struct XcdHint {
+    uint32_t off;      // expected XCD of workgroup 0
+    uint32_t *report;  // pinned host word for workgroup 0's XCD (0x100 | xcd), or null
+};
+
+__device__ __forceinline__ int wg_xcd(int wg, const XcdHint &h) { return (int)(((uint32_t)wg + h.off) % kNumXcd); }
+
+// Workgroup 0 reports the XCD it runs on (a vector store to pinned host memory).
+__device__ __forceinline__ void report_xcd(const XcdHint &h) {
+    if (h.report != nullptr && blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(h.report, 0x100u | hw_xcc_id(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Logical placement of workgroup `wg` in a grid whose size is a multiple of 8: it runs on XCD
+// wg_xcd(wg); `slice` is the data slice it serves, `rank` its index among the workgroups of
+// its XCD (a bijection of the grid onto slices x ranks for any offset).
 struct XcdSlot {
     int slice;    // which 1/8 of the data
     int rank;     // workgroup index within the XCD
     int per_xcd;  // workgroups per XCD
 };
 
-__device__ __forceinline__ XcdSlot xcd_slot(int wg, int grid, int mode, unsigned rot) {
+__device__ __forceinline__ XcdSlot xcd_slot(int wg, int grid, int mode, unsigned rot, const XcdHint &h) {
     XcdSlot s;
     s.per_xcd = grid / kNumXcd;
     s.rank = wg / kNumXcd;
-    int xcd = wg % kNumXcd;
+    const int xcd = wg_xcd(wg, h);
     s.slice = (mode == XD_MODE_ROTATED) ? (int)((xcd + rot) % kNumXcd) : xcd;
     return s;
 }
@@ -163,8 +184,18 @@ __device__ __forceinline__ StagedHome stage_home_nosync(const HomeMap &h, uint64
     return sh;
 }
 
-// Die next to the XCD that workgroup `wg` runs on (round-robin dispatch: XCD = wg mod 8).
-__device__ __forceinline__ uint32_t wg_die(int wg) { return (uint32_t)((wg % kNumXcd) >= kNumXcd / 2); }
+// Die next to the XCD that workgroup `wg` runs on (XCDs 0-3: die 0), and the workgroup's index
+// among the grid's workgroups on that die (a bijection of the grid onto dies x ranks for any
+// offset, the grid a multiple of 8).
+__device__ __forceinline__ uint32_t wg_die(int wg, const XcdHint &h) { return (uint32_t)(wg_xcd(wg, h) >= kNumXcd / 2); }
+__device__ __forceinline__ int die_rank(int wg, const XcdHint &h) {
+    return (wg / kNumXcd) * (kNumXcd / 2) + wg_xcd(wg, h) % (kNumXcd / 2);
+}
+
+// host: the placement hint of `stream` on the current device (xd_core.hip); the noalloc form
+// never allocates the stream's pinned report word (no report until another call made it)
+XcdHint xcd_hint(hipStream_t stream);
+XcdHint xcd_hint_noalloc(hipStream_t stream);
 
 uint64_t home_mask();  // host: the current mask (xd_set_home_mask)
 

@@ -4,6 +4,7 @@
 #include <atomic>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <utility>
@@ -36,6 +37,51 @@ unsigned next_rotation(int passes) {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
     return g_rotation[dev].fetch_add((unsigned)passes) + 1u;
 }
+
+// ---- placement hints: one pinned word per (device, stream), written by workgroup 0 of every
+// dispatch that takes a hint, read by the next launch on the stream ----
+namespace {
+std::mutex g_hint_mu;
+std::map<std::pair<int, uintptr_t>, uint32_t *> g_hint_slots;
+uint32_t *g_hint_block = nullptr;
+int g_hint_used = 0;
+constexpr int kHintBlockWords = 1024;      // one 4 KiB pinned block per 1024 streams
+constexpr size_t kMaxHintSlots = 16384;    // streams beyond this get no slot (offset 0)
+}  // namespace
+
+static uint32_t *hint_slot(hipStream_t s, bool create) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_hint_mu);
+    const auto key = std::make_pair(dev, reinterpret_cast<uintptr_t>(s));
+    const auto it = g_hint_slots.find(key);
+    if (it != g_hint_slots.end()) return it->second;
+    if (!create || g_hint_slots.size() >= kMaxHintSlots) return nullptr;
+    if (g_hint_block == nullptr || g_hint_used == kHintBlockWords) {
+        void *p = nullptr;
+        if (hipHostMalloc(&p, kHintBlockWords * sizeof(uint32_t), hipHostMallocCoherent) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        std::memset(p, 0, kHintBlockWords * sizeof(uint32_t));
+        g_hint_block = static_cast<uint32_t *>(p);
+        g_hint_used = 0;
+    }
+    uint32_t *w = g_hint_block + g_hint_used++;
+    g_hint_slots.emplace(key, w);
+    return w;
+}
+
+static XcdHint hint_of(uint32_t *w) {
+    const uint32_t v = w ? __atomic_load_n(w, __ATOMIC_RELAXED) : 0u;
+    return XcdHint{(v & 0x100u) ? (v & (kNumXcd - 1u)) : 0u, w};
+}
+
+XcdHint xcd_hint(hipStream_t stream) { return hint_of(hint_slot(stream, true)); }
+XcdHint xcd_hint_noalloc(hipStream_t stream) { return hint_of(hint_slot(stream, false)); }
 
 static std::atomic<uint64_t> g_home_mask{kDefaultHomeMask};
 uint64_t home_mask() { return g_home_mask.load(std::memory_order_relaxed); }
@@ -114,7 +160,8 @@ constexpr int kStreamThreads = 256;
 
 template <int kStreamPairsInFlight>
 __global__ void __launch_bounds__(kStreamThreads)
-read_stream_kernel(const u32x4 *buf, uint64_t nvec, uint64_t npairs, int mode, HomeMap home) {
+read_stream_kernel(const u32x4 *buf, uint64_t nvec, uint64_t npairs, int mode, HomeMap home, XcdHint xh) {
+    report_xcd(xh);
     __shared__ uint8_t lattr[2048];  // the buffer's home map (buffers up to 4 GiB)
     const StagedHome hs = stage_home_nosync(home, reinterpret_cast<uint64_t>(buf), nvec * 16, lattr, 2048,
                                             mode != XD_MODE_OBLIVIOUS && npairs != 0);
@@ -135,8 +182,8 @@ read_stream_kernel(const u32x4 *buf, uint64_t nvec, uint64_t npairs, int mode, H
     } else {
         const int b = (int)blockIdx.x;
         const uint64_t per_die = gridDim.x / 2;
-        const uint64_t rank = (uint64_t)(b / kNumXcd) * (kNumXcd / 2) + (uint64_t)(b % (kNumXcd / 2));
-        const uint32_t want = mode == XD_MODE_AWARE ? wg_die(b) : (wg_die(b) ^ 1u);
+        const uint64_t rank = (uint64_t)die_rank(b, xh);
+        const uint32_t want = mode == XD_MODE_AWARE ? wg_die(b, xh) : (wg_die(b, xh) ^ 1u);
         const uint64_t base = reinterpret_cast<uint64_t>(buf);
         constexpr uint64_t kChunkVec = kHomeChunk / 16;  // 512 vectors, two per thread
         for (uint64_t p0 = rank; p0 < npairs; p0 += per_die * kStreamPairsInFlight) {
@@ -189,10 +236,12 @@ __device__ __forceinline__ uint32_t *home_probe_word(uint64_t page0, uint64_t p,
 }
 
 // Workgroups on XCD 2 load the probe words first, so that both timed passes find the lines
-// in the Infinity Cache rather than one of them paying the HBM miss.
+// in the Infinity Cache rather than one of them paying the HBM miss. (Roles by the XCD read
+// from the hardware; workgroup b of each XCD takes pages b / 8, b / 8 + W, ...: with the
+// round-robin dispatch every XCD holds one workgroup of each b / 8.)
 __global__ void home_touch_kernel(uint64_t page0, uint64_t npages, uint64_t lo, uint64_t hi, uint32_t *sink) {
     const int b = (int)blockIdx.x;
-    if (b % kNumXcd != 2 || threadIdx.x != 0) return;
+    if (hw_xcc_id() != 2u || threadIdx.x != 0) return;
     uint32_t acc = 0;
     for (uint64_t p = (uint64_t)(b / kNumXcd); p < npages; p += kHomeProbeWgsPerXcd)
         for (int k = 0; k < kHomeProbeLines; ++k) {
@@ -207,8 +256,7 @@ __global__ void home_touch_kernel(uint64_t page0, uint64_t npages, uint64_t lo, 
 __global__ void home_measure_kernel(uint64_t page0, uint64_t npages, uint64_t lo, uint64_t hi, uint32_t *lat,
                                     int die) {
     const int b = (int)blockIdx.x;
-    const int x = b % kNumXcd;
-    if (x != 4 * die || threadIdx.x != 0) return;
+    if (hw_xcc_id() != (uint32_t)(4 * die) || threadIdx.x != 0) return;
     for (uint64_t p = (uint64_t)(b / kNumXcd); p < npages; p += kHomeProbeWgsPerXcd) {
         uint32_t best = 0xffffffffu;
         for (int k = 0; k < kHomeProbeLines; ++k) {
@@ -290,6 +338,12 @@ int xd_domain_scan(int num_wg, uint32_t *out_placement, void *stream) {
     return launch_status("domain_scan_kernel");
 }
 
+int xd_xcd_offset(void *stream) {
+    uint32_t *w = hint_slot(static_cast<hipStream_t>(stream), false);
+    const uint32_t v = w ? __atomic_load_n(w, __ATOMIC_RELAXED) : 0u;
+    return (v & 0x100u) ? (int)(v & (kNumXcd - 1u)) : -1;
+}
+
 uint64_t xd_home_mask(void) { return home_mask(); }
 
 int xd_set_home_mask(uint64_t mask) {
@@ -363,11 +417,12 @@ int xd_read_stream(const void *buf, size_t bytes, int mode, const uint8_t *home_
     const u32x4 *b16 = reinterpret_cast<const u32x4 *>(buf);
     const uint64_t np = pairs ? (uint64_t)(bytes / (2 * kHomeChunk)) : 0ull;
     hipStream_t s = (hipStream_t)stream;
+    const XcdHint xh = xcd_hint(s);
     switch (depth) {
-        case 1: launch("read_stream_kernel", read_stream_kernel<1>, dim3(grid), dim3(kStreamThreads), 0, s, b16, nvec, np, mode, home); break;
-        case 2: launch("read_stream_kernel", read_stream_kernel<2>, dim3(grid), dim3(kStreamThreads), 0, s, b16, nvec, np, mode, home); break;
-        case 8: launch("read_stream_kernel", read_stream_kernel<8>, dim3(grid), dim3(kStreamThreads), 0, s, b16, nvec, np, mode, home); break;
-        default: launch("read_stream_kernel", read_stream_kernel<4>, dim3(grid), dim3(kStreamThreads), 0, s, b16, nvec, np, mode, home); break;
+        case 1: launch("read_stream_kernel", read_stream_kernel<1>, dim3(grid), dim3(kStreamThreads), 0, s, b16, nvec, np, mode, home, xh); break;
+        case 2: launch("read_stream_kernel", read_stream_kernel<2>, dim3(grid), dim3(kStreamThreads), 0, s, b16, nvec, np, mode, home, xh); break;
+        case 8: launch("read_stream_kernel", read_stream_kernel<8>, dim3(grid), dim3(kStreamThreads), 0, s, b16, nvec, np, mode, home, xh); break;
+        default: launch("read_stream_kernel", read_stream_kernel<4>, dim3(grid), dim3(kStreamThreads), 0, s, b16, nvec, np, mode, home, xh); break;
     }
     return launch_status("read_stream_kernel");
 }

@@ -51,14 +51,15 @@ __device__ __forceinline__ float dot16_f16(uint4 a, uint4 b, float acc) {
 template <bool F16, int U>
 __global__ void __launch_bounds__(kGemvThreads)
 gemv_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__restrict__ y, int M, int nv,
-            int rows_per_wg, int nchunks, int mode, unsigned rot) {
+            int rows_per_wg, int nchunks, int mode, unsigned rot, XcdHint xh) {
     extern __shared__ uint4 xs[];
+    report_xcd(xh);
     const int b = (int)blockIdx.x;
     int chunk;
     if (mode == XD_MODE_OBLIVIOUS) {
         chunk = b;
     } else {
-        XcdSlot s = xcd_slot(b, (int)gridDim.x, mode, rot);
+        XcdSlot s = xcd_slot(b, (int)gridDim.x, mode, rot, xh);
         chunk = s.slice * s.per_xcd + s.rank;
     }
     if (chunk >= nchunks) return;  // whole workgroup leaves before any barrier
@@ -99,7 +100,8 @@ gemv_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__r
 template <bool F16, int CW, int S, bool DB>
 __global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4)))
 gemv_exact_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__restrict__ y, int M,
-                  int rows_per_wg, int nchunks, int mode, unsigned rot) {
+                  int rows_per_wg, int nchunks, int mode, unsigned rot, XcdHint xh) {
+    report_xcd(xh);
     constexpr int nv = kWave * CW * S;
     constexpr int kRowsPerPass = kGemvWaves / S;
     __shared__ float part[kGemvWaves];
@@ -108,7 +110,7 @@ gemv_exact_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, floa
     if (mode == XD_MODE_OBLIVIOUS) {
         chunk = b;
     } else {
-        XcdSlot sl = xcd_slot(b, (int)gridDim.x, mode, rot);
+        XcdSlot sl = xcd_slot(b, (int)gridDim.x, mode, rot, xh);
         chunk = sl.slice * sl.per_xcd + sl.rank;
     }
     if (chunk >= nchunks) return;
@@ -189,13 +191,14 @@ gemv_exact_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, floa
 template <bool F16, int CW>
 __global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4)))
 gemv_rowhome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__restrict__ y, int M,
-                    int mode, HomeMap home) {
+                    int mode, HomeMap home, XcdHint xh) {
+    report_xcd(xh);
     constexpr int nv = kWave * CW;
     constexpr int kGroup = 8;
     const int b = (int)blockIdx.x;
     const int per_die = (int)gridDim.x / 2;
-    const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
-    const uint32_t die = wg_die(b);
+    const int rank = die_rank(b, xh);
+    const uint32_t die = wg_die(b, xh);
     const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
     const int wave = (int)threadIdx.x / kWave;
     const int lane = (int)threadIdx.x % kWave;
@@ -275,14 +278,15 @@ __device__ __forceinline__ void seg_meet(float part, int j, int row, int seg, in
 template <bool F16, bool PAIR>
 __global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4)))
 gemv_seghome_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__restrict__ y, int M, int S,
-                    int mode, HomeMap home, uint32_t *__restrict__ cnt, uint32_t *__restrict__ slot) {
+                    int mode, HomeMap home, uint32_t *__restrict__ cnt, uint32_t *__restrict__ slot, XcdHint xh) {
+    report_xcd(xh);
     constexpr int CW = 8;
     constexpr int kSegVec = kWave * CW;  // 512 vectors = 8 KiB
     constexpr int kGroup = 8;
     const int b = (int)blockIdx.x;
     const int per_die = (int)gridDim.x / 2;
-    const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
-    const uint32_t die = wg_die(b);
+    const int rank = die_rank(b, xh);
+    const uint32_t die = wg_die(b, xh);
     const uint32_t want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
     const int wave = (int)threadIdx.x / kWave;
     const int lane = (int)threadIdx.x % kWave;
@@ -398,6 +402,7 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
     unsigned rot = mode == XD_MODE_ROTATED ? next_rotation(1) % kNumXcd : 0u;
     if (mode == XD_MODE_ROTATED && rot == 0) rot = 1;
     hipStream_t s = (hipStream_t)stream;
+    const XcdHint xh = xcd_hint(s);
     const uint4 *A4 = reinterpret_cast<const uint4 *>(A);
     const uint4 *x4 = reinterpret_cast<const uint4 *>(x);
     bool done = false;
@@ -416,10 +421,10 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
         if (sgrid > (1LL << 30)) return fail(XD_ERR_UNSUPPORTED, "gemv: matrix too large for the split-row route");
         if (S == 2)
             launch("gemv_seghome_kernel", gemv_seghome_kernel<F16, true>, dim3((unsigned)sgrid), dim3(kGemvThreads), 0, s, A4, x4,
-                               y, M, S, mode, home, cnt, slot);
+                               y, M, S, mode, home, cnt, slot, xh);
         else
             launch("gemv_seghome_kernel", gemv_seghome_kernel<F16, false>, dim3((unsigned)sgrid), dim3(kGemvThreads), 0, s, A4,
-                               x4, y, M, S, mode, home, cnt, slot);
+                               x4, y, M, S, mode, home, cnt, slot, xh);
         done = true;
     }
     // Memory-home routing when every row sits inside one 8 KiB chunk.
@@ -435,7 +440,7 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
 #define XD_GEMV_HOME(CC)                                                                                       \
     if (CW == CC) {                                                                                           \
         launch("gemv_rowhome_kernel", gemv_rowhome_kernel<F16, CC>, dim3(hgrid), dim3(kGemvThreads), 0, s, A4, x4, y, M, \
-                           mode, home);                                                                        \
+                           mode, home, xh);                                                                        \
     } else
         XD_GEMV_HOME(1)
         XD_GEMV_HOME(2)
@@ -454,7 +459,7 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
 #define XD_GEMV_EXACT(CC, SS, DBB)                                                                        \
     if (CW == CC && S == SS) {                                                                          \
         launch("gemv_exact_kernel", gemv_exact_kernel<F16, CC, SS, DBB>, dim3(grid), dim3(kGemvThreads), 0, s, A4, \
-                           x4, y, M, rpw, nchunks, mode, rot);                                          \
+                           x4, y, M, rpw, nchunks, mode, rot, xh);                                          \
     } else
         XD_GEMV_EXACT(1, 1, true)
         XD_GEMV_EXACT(2, 1, true)
@@ -478,10 +483,10 @@ static int launch_gemv(const void *A, const void *x, float *y, int M, int K, int
     if (!done) {
         if (nv >= kWave * 16) {
             launch("gemv_kernel", gemv_kernel<F16, 16>, dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
-                               nchunks, mode, rot);
+                               nchunks, mode, rot, xh);
         } else {
             launch("gemv_kernel", gemv_kernel<F16, 8>, dim3(grid), dim3(kGemvThreads), lds, s, A4, x4, y, M, nv, rpw,
-                               nchunks, mode, rot);
+                               nchunks, mode, rot, xh);
         }
     }
     return launch_status("gemv_kernel");

@@ -41,7 +41,8 @@ struct Walk {
     uint32_t want;           // die whose items this wave takes (home modes)
 };
 
-__device__ __forceinline__ Walk make_walk(int mode) {
+__device__ __forceinline__ Walk make_walk(int mode, const XcdHint &xh) {
+    report_xcd(xh);
     Walk w;
     const int b = (int)blockIdx.x;
     const int wave = (int)threadIdx.x / kWave;
@@ -52,10 +53,10 @@ __device__ __forceinline__ Walk make_walk(int mode) {
         w.want = 0;
     } else {
         const int per_die = (int)gridDim.x / 2;
-        const int rank = (b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2));
+        const int rank = die_rank(b, xh);
         w.first = (uint64_t)rank * kWavesPerWg + wave;
         w.stride = (uint64_t)per_die * kWavesPerWg;
-        const uint32_t die = wg_die(b);
+        const uint32_t die = wg_die(b, xh);
         w.want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
     }
     return w;
@@ -122,11 +123,11 @@ __device__ __forceinline__ void for_each_owned(const Walk &w, uint64_t n, bool f
 __global__ void __launch_bounds__(kHashThreads)
 hash_insert_kernel(Slot *__restrict__ table, uint64_t mask, const uint64_t *__restrict__ keys,
                    const uint64_t *__restrict__ vals, uint64_t n, int mode, HomeMap home,
-                   unsigned long long *__restrict__ failed) {
+                   unsigned long long *__restrict__ failed, XcdHint xh) {
     __shared__ uint32_t qidx[kHashThreads / kWave][2 * kWave];
     __shared__ uint64_t qkey[kHashThreads / kWave][2 * kWave];
     __shared__ uint8_t lattr[kLdsPages];
-    const Walk w = make_walk(mode);
+    const Walk w = make_walk(mode, xh);
     const bool filter = mode != XD_MODE_OBLIVIOUS;
     const uint64_t base = reinterpret_cast<uint64_t>(table);
     const SlotHome sh = stage_home(home, base, (mask + 1) * sizeof(Slot), lattr, filter);
@@ -142,11 +143,12 @@ hash_insert_kernel(Slot *__restrict__ table, uint64_t mask, const uint64_t *__re
 
 __global__ void __launch_bounds__(kHashThreads)
 hash_lookup_kernel(const Slot *__restrict__ table, uint64_t mask, const uint64_t *__restrict__ queries, uint64_t n,
-                   int mode, HomeMap home, uint64_t *__restrict__ vals_out, uint8_t *__restrict__ found_out) {
+                   int mode, HomeMap home, uint64_t *__restrict__ vals_out, uint8_t *__restrict__ found_out,
+                   XcdHint xh) {
     __shared__ uint32_t qidx[kHashThreads / kWave][2 * kWave];
     __shared__ uint64_t qkey[kHashThreads / kWave][2 * kWave];
     __shared__ uint8_t lattr[kLdsPages];
-    const Walk w = make_walk(mode);
+    const Walk w = make_walk(mode, xh);
     const bool filter = mode != XD_MODE_OBLIVIOUS;
     const uint64_t base = reinterpret_cast<uint64_t>(table);
     const SlotHome sh = stage_home(home, base, (mask + 1) * sizeof(Slot), lattr, filter);
@@ -220,11 +222,11 @@ __device__ __forceinline__ int32_t dep_probe_one(const int2 *__restrict__ table,
 
 __global__ void __launch_bounds__(kHashThreads)
 dep_probe_kernel(const int2 *__restrict__ table, uint32_t mask, const int32_t *__restrict__ queries, uint64_t n,
-                 int chain_len, int32_t *__restrict__ out, int mode, HomeMap home) {
+                 int chain_len, int32_t *__restrict__ out, int mode, HomeMap home, XcdHint xh) {
     __shared__ uint32_t qidx[kHashThreads / kWave][2 * kWave];
     __shared__ uint64_t qkey[kHashThreads / kWave][2 * kWave];
     __shared__ uint8_t lattr[kLdsPages];
-    const Walk w = make_walk(mode);
+    const Walk w = make_walk(mode, xh);
     const bool filter = mode != XD_MODE_OBLIVIOUS;
     const uint64_t base = reinterpret_cast<uint64_t>(table);
     const SlotHome sh = stage_home(home, base, ((uint64_t)mask + 1) * sizeof(int2), lattr, filter);
@@ -380,7 +382,8 @@ route_scatter_kernel(uint32_t mask, const int32_t *__restrict__ queries, uint64_
 __global__ void __launch_bounds__(kHashThreads)
 dep_probe_routed_kernel(const int2 *__restrict__ table, uint32_t mask, const int2 *__restrict__ entries,
                         const unsigned long long *__restrict__ header, int chain_len, int32_t *__restrict__ out,
-                        int mode) {
+                        int mode, XcdHint xh) {
+    report_xcd(xh);
     const uint64_t n0 = header[0], n = header[1];
     const int b = (int)blockIdx.x;
     uint64_t first, end, rank, nwg;
@@ -390,11 +393,11 @@ dep_probe_routed_kernel(const int2 *__restrict__ table, uint32_t mask, const int
         rank = (uint64_t)b;
         nwg = gridDim.x;
     } else {
-        const uint32_t die = wg_die(b);
+        const uint32_t die = wg_die(b, xh);
         const uint32_t list = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
         first = list ? n0 : 0;
         end = list ? n : n0;
-        rank = (uint64_t)((b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2)));
+        rank = (uint64_t)die_rank(b, xh);
         nwg = gridDim.x / 2;
     }
     for (uint64_t idx = first + rank * kHashThreads + threadIdx.x; idx < end; idx += nwg * kHashThreads) {
@@ -480,7 +483,8 @@ int xd_hash_insert_u64(void *table, uint64_t slots, const uint64_t *keys, const 
     if (n == 0) return XD_OK;
     launch("hash_insert_kernel", hash_insert_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<Slot *>(table), slots - 1, keys, vals, n, mode,
-                       HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()}, failed);
+                       HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()}, failed,
+                       xcd_hint((hipStream_t)stream));
     return launch_status("hash_insert_kernel");
 }
 
@@ -495,7 +499,7 @@ int xd_hash_lookup_u64(const void *table, uint64_t slots, const uint64_t *querie
     launch("hash_lookup_kernel", hash_lookup_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<const Slot *>(table), slots - 1, queries, n, mode,
                        HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()}, vals_out,
-                       found_out);
+                       found_out, xcd_hint((hipStream_t)stream));
     return launch_status("hash_lookup_kernel");
 }
 
@@ -510,7 +514,8 @@ int xd_dep_probe(const void *table, uint64_t slots, const int32_t *queries, uint
     if (n == 0) return XD_OK;
     launch("dep_probe_kernel", dep_probe_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<const int2 *>(table), (uint32_t)(slots - 1), queries, n, chain_len, out, mode,
-                       HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()});
+                       HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()},
+                       xcd_hint((hipStream_t)stream));
     return launch_status("dep_probe_kernel");
 }
 
@@ -559,7 +564,7 @@ int xd_dep_probe_routed(const void *table, uint64_t slots, const void *route, ui
     launch("dep_probe_routed_kernel", dep_probe_routed_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<const int2 *>(table), (uint32_t)(slots - 1),
                        reinterpret_cast<const int2 *>(r + L.entries), reinterpret_cast<const unsigned long long *>(r),
-                       chain_len, out, mode);
+                       chain_len, out, mode, xcd_hint((hipStream_t)stream));
     return launch_status("dep_probe_routed_kernel");
 }
 

@@ -240,8 +240,10 @@ hb_split_kernel(SplitSrc src, BuildGeom g, int shift, int nbits, SplitDst dst) {
 // Build pass: one workgroup per range (see the file comment for the placement).
 __global__ void __launch_bounds__(kBuildThreads)
 hb_build_kernel(BuildGeom g, int mode, const Slot *__restrict__ reg, const uint32_t *__restrict__ cur, uint64_t cap,
-                Slot *__restrict__ table, Slot *__restrict__ spill, uint32_t *__restrict__ spill_cnt, SplitDst ovf) {
+                Slot *__restrict__ table, Slot *__restrict__ spill, uint32_t *__restrict__ spill_cnt, SplitDst ovf,
+                XcdHint xh) {
     __shared__ __attribute__((aligned(16))) Slot tab[kRange];
+    report_xcd(xh);
     __shared__ uint32_t s_nsp;
     __shared__ uint8_t lattr[kBuildLdsPages];
     const int tid = (int)threadIdx.x;
@@ -250,9 +252,9 @@ hb_build_kernel(BuildGeom g, int mode, const Slot *__restrict__ reg, const uint3
     if (!g.die) {
         r = (uint32_t)b;
     } else {
-        const uint32_t die = wg_die(b);
+        const uint32_t die = wg_die(b, xh);
         const uint32_t want = mode == XD_MODE_AWARE ? die : (die ^ 1u);
-        const uint32_t rank = (uint32_t)((b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2)));
+        const uint32_t rank = (uint32_t)die_rank(b, xh);
         r = 2u * rank + want;
     }
     for (uint32_t j = (uint32_t)tid; j < kRange; j += kBuildThreads) tab[j] = Slot{kEmpty, 0};
@@ -475,7 +477,7 @@ int xd_hash_build_u64(void *table, uint64_t slots, const uint64_t *keys, const u
 
     launch("hb_build_kernel", hb_build_kernel, dim3(L.nr), dim3(kBuildThreads), 0, s, g, mode,
            static_cast<const Slot *>(regB), static_cast<const uint32_t *>(curB), L.capB, static_cast<Slot *>(table), spill,
-           spill_cnt, dB);
+           spill_cnt, dB, xcd_hint(s));
     if (int rc = launch_status("hb_build_kernel")) return rc;
 
     const uint64_t max_probe = slots < kMaxProbe ? slots : kMaxProbe;

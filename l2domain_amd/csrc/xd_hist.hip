@@ -283,6 +283,7 @@ struct PartSrc {
     uint64_t npairs;       // routed: pairs in all groups (the last group may be short)
     int mode;              // routed: XD_MODE_AWARE (near chunks) or XD_MODE_ROTATED (far chunks)
     HomeMap home;          // routed
+    XcdHint xh;            // routed: workgroup -> XCD placement
 };
 
 // PACK (at most kPackBuckets buckets, full and routed kinds): each counter column takes one
@@ -320,9 +321,10 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
         // Routed: group i's pairs each hold one 8 KiB chunk on either I/O die; tile 2i + d
         // is the group's chunks homed on die d, read by a workgroup of die d (aware) or of
         // the other die (rotated). The grid holds at least `groups` workgroups per die.
-        grp = (g / kNumXcd) * (kNumXcd / 2) + g % (kNumXcd / 2);
+        report_xcd(src.xh);
+        grp = die_rank(g, src.xh);
         if (grp >= src.groups) return;
-        want = src.mode == XD_MODE_AWARE ? wg_die(g) : (wg_die(g) ^ 1u);
+        want = src.mode == XD_MODE_AWARE ? wg_die(g, src.xh) : (wg_die(g, src.xh) ^ 1u);
         t = 2 * grp + (int)want;
     } else {
         t = src.tile0 + g;
@@ -625,9 +627,10 @@ hist_partition_lean_kernel(PartSrc src, uint32_t bound, int nb, uint16_t *__rest
     int grp = 0;
     if (KIND == kPartRouted) {
         // as partition_tile: tile 2i + d is group i's chunks homed on die d
-        grp = (g / kNumXcd) * (kNumXcd / 2) + g % (kNumXcd / 2);
+        report_xcd(src.xh);
+        grp = die_rank(g, src.xh);
         if (grp >= src.groups) return;
-        want = src.mode == XD_MODE_AWARE ? wg_die(g) : (wg_die(g) ^ 1u);
+        want = src.mode == XD_MODE_AWARE ? wg_die(g, src.xh) : (wg_die(g, src.xh) ^ 1u);
         t = 2 * grp + (int)want;
     } else {
         t = src.tile0 + g;
@@ -904,7 +907,7 @@ __global__ void __launch_bounds__(kP2Threads)
 hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb, int ntiles,
                   const uint32_t *__restrict__ tot, int per_xcd, uint32_t *__restrict__ partials,
                   HistBucket *__restrict__ buckets, int mode, unsigned rot, uint32_t *__restrict__ hot_tab,
-                  const uint32_t *__restrict__ hot_part) {
+                  const uint32_t *__restrict__ hot_part, XcdHint xh) {
     __shared__ __attribute__((aligned(16))) uint32_t h[kCountSlots];
     __shared__ uint32_t wsum[kP2Waves];
     __shared__ int s_item[3];  // bucket (-1: idle slot), t0, t1
@@ -915,7 +918,7 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     if (mode == XD_MODE_OBLIVIOUS) {
         slot = g;
     } else {
-        XcdSlot s = xcd_slot(g, (int)gridDim.x, mode, rot);
+        XcdSlot s = xcd_slot(g, (int)gridDim.x, mode, rot, xh);
         slot = s.slice * per_xcd + s.rank;
     }
     if (tid == 0) s_item[0] = -1;
@@ -1186,6 +1189,7 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     if (workspace == nullptr || workspace_bytes < L.total || !aligned16(workspace))
         return fail(XD_ERR_WORKSPACE, "xd_hist_u32: workspace missing, misaligned or smaller than xd_hist_workspace_size()");
     hipStream_t s = (hipStream_t)stream;
+    const XcdHint xh = xcd_hint(s);
     char *ws = static_cast<char *>(workspace);
     uint16_t *part = reinterpret_cast<uint16_t *>(ws + L.part);
     uint32_t *offs = reinterpret_cast<uint32_t *>(ws + L.offs);
@@ -1214,12 +1218,12 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
         const size_t vend = aligned16(keys + r0) ? r0 + (r1 - r0) / 4 * 4 : r0;
         if (vend > r0) {
             const size_t nt = (vend - r0 + kTileKeys - 1) / kTileKeys;
-            plan[nplan++] = PartLaunch{kPartFull, PartSrc{keys, r0, vend, ntl, 0, 0, 0, 0, home}, (unsigned)nt};
+            plan[nplan++] = PartLaunch{kPartFull, PartSrc{keys, r0, vend, ntl, 0, 0, 0, 0, home, XcdHint{0u, nullptr}}, (unsigned)nt};
             ntl += (int)nt;
         }
         if (vend < r1) {
             const size_t nt = (r1 - vend + kTileKeys - 1) / kTileKeys;
-            plan[nplan++] = PartLaunch{kPartRange, PartSrc{keys, vend, r1, ntl, 0, 0, 0, 0, home}, (unsigned)nt};
+            plan[nplan++] = PartLaunch{kPartRange, PartSrc{keys, vend, r1, ntl, 0, 0, 0, 0, home, XcdHint{0u, nullptr}}, (unsigned)nt};
             ntl += (int)nt;
         }
     };
@@ -1235,7 +1239,7 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
             const size_t head = (size_t)(pfirst * 16384 - A) / 4;
             const size_t tail0 = head + (size_t)npairs * 4096;
             const unsigned grid = (unsigned)((groups + kNumXcd / 2 - 1) / (kNumXcd / 2) * kNumXcd);
-            plan[nplan++] = PartLaunch{kPartRouted, PartSrc{keys, 0, 0, 0, (int)groups, pfirst, npairs, mode, home}, grid};
+            plan[nplan++] = PartLaunch{kPartRouted, PartSrc{keys, 0, 0, 0, (int)groups, pfirst, npairs, mode, home, xh}, grid};
             ntl = 2 * (int)groups;
             if (head > 0) contiguous(0, head);
             if (tail0 < n) contiguous(tail0, n);
@@ -1281,7 +1285,7 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
         if (int rc = launch_status("hist_partition_kernel")) return rc;
     }
     launch("hist_count_kernel", hist_count_kernel, dim3(L.nitems), dim3(kP2Threads), 0, s, part, offs, L.nb, ntl, tot,
-           L.per_xcd, partials, buckets, mode, rot_eff, hot, hot_part);
+           L.per_xcd, partials, buckets, mode, rot_eff, hot, hot_part, xh);
     if (int rc = launch_status("hist_count_kernel")) return rc;
     // one workgroup per merge unit, up to 4096
     const int merge_grid = std::min(std::max(L.nb * kMergeUnitsPerBucket, kNumXcd * 64), 4096);

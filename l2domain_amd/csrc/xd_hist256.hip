@@ -106,7 +106,8 @@ __device__ __forceinline__ uint4 h8_load(const uint4 *__restrict__ words4, uint6
 __global__ void __launch_bounds__(kH8Threads)
 hist256_kernel(const uint32_t *__restrict__ words, uint64_t n, uint64_t pair0, uint64_t npairs, int mode,
                HomeMap home, unsigned long long *__restrict__ acc, uint32_t *__restrict__ sync,
-               uint32_t *__restrict__ counts) {
+               uint32_t *__restrict__ counts, XcdHint xh) {
+    report_xcd(xh);
     __shared__ __attribute__((aligned(16))) uint32_t h[kH8Bins * kWave];
     __shared__ uint8_t lattr[kH8MaxPages];
     __shared__ uint32_t s_last;
@@ -131,9 +132,9 @@ hist256_kernel(const uint32_t *__restrict__ words, uint64_t n, uint64_t pair0, u
         first = (uint64_t)b;
         step = (uint64_t)grid;
     } else {
-        first = (uint64_t)((b / kNumXcd) * (kNumXcd / 2) + (b % (kNumXcd / 2)));
+        first = (uint64_t)die_rank(b, xh);
         step = (uint64_t)(grid / 2);
-        const uint32_t die = wg_die(b);
+        const uint32_t die = wg_die(b, xh);
         want = (mode == XD_MODE_AWARE) ? die : (die ^ 1u);
     }
     const uint64_t npm = first < npairs ? (npairs - first + step - 1) / step : 0;
@@ -321,7 +322,7 @@ static int hist256_run(const uint32_t *words, size_t n, uint32_t *counts, int mo
     const HomeMap home{home_attr, wbeg / kHomePage, home_mask()};
     launch(timed ? "hist256_kernel" : nullptr, hist256_kernel, dim3(grid), dim3(kH8Threads), 0, s, words, (uint64_t)n,
            pair0, npairs, mode, home, reinterpret_cast<unsigned long long *>(ws + L.acc),
-           reinterpret_cast<uint32_t *>(ws + L.sync), counts);
+           reinterpret_cast<uint32_t *>(ws + L.sync), counts, timed ? xcd_hint(s) : xcd_hint_noalloc(s));
     return launch_status("hist256_kernel");
 }
 

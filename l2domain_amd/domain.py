@@ -35,6 +35,12 @@ def domain_scan(num_wg: int, device: int = 0) -> torch.Tensor:
     return out.cpu().view(torch.int32)
 
 
+def xcd_offset(stream: torch.cuda.Stream | None = None) -> int:
+    """XCD of workgroup 0 in the last dispatch of the library's kernels on `stream` (workgroup
+    i then ran on XCD (i + offset) mod 8), or -1 if none has run on it yet."""
+    return int(_lib.lib.xd_xcd_offset(stream_handle(stream)))
+
+
 class CacheFlusher:
     """Owns the read-stream buffer used to evict the L2s and the Infinity Cache."""
 

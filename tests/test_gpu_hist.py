@@ -179,3 +179,22 @@ def test_config_2p28_zipf(config_keys, mode):
     got = counts.cpu().numpy().view(np.uint32)
     assert int(got.astype(np.uint64).sum()) == HIST_KEYS
     np.testing.assert_array_equal(got, ref)
+
+
+def test_aware_on_queues_that_start_elsewhere():
+    """The placement offset only moves work between XCDs: on new streams (whose queues may
+    deal workgroup 0 to another XCC), before and after the library has learned the offset,
+    every mode is bit-exact."""
+    n = (1 << 22) + 4099
+    k = gen.zipf_keys_device(n, 1 << 20, 81, ZIPF_S).cpu().numpy().view(np.uint32).copy()
+    ref, _ = ora.histogram(k, 1 << 20)
+    h = Histogram(n, 1 << 20)
+    keys = torch.from_numpy(k.view(np.int32)).cuda()
+    for s in [torch.cuda.Stream() for _ in range(6)]:
+        for mode in ("aware", "rotated", "aware"):
+            counts = torch.full((1 << 20,), -7, dtype=torch.int32, device="cuda")
+            torch.cuda.synchronize()  # keys, workspace and counts written on the default stream
+            h(keys, counts, mode=mode, stream=s)
+            s.synchronize()
+            np.testing.assert_array_equal(counts.cpu().numpy().view(np.uint32), ref)
+

@@ -49,19 +49,19 @@ MODES = ("oblivious", "aware", "rotated")
 # costs a request each way).
 TRAFFIC_SRC = "profiles/traffic_by_config.md (FETCH_SIZE/WRITE_SIZE runs of the commit named there)"
 TRAFFIC = {
-    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1311132384,
-    ("hash_2p26_lf0.5_u64", "warm", "aware"): 20178078655,
-    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 544238636,
-    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 544587674,
-    ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 246375344,
-    ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3931995586,
-    ("bfs_rmat22_ef16", "warm", "aware"): 238988530,
-    ("gemv_f32_4096x4096", "warm", "aware"): 67747047,
-    ("gemv_f32_4096x4096", "cold", "aware"): 67747990,
-    ("gemv_f16_14336x4096", "warm", "aware"): 117648928,
-    ("gemv_f16_14336x4096", "cold", "aware"): 117650360,
-    ("gemv_f16_4096x14336", "warm", "aware"): 118187405,
-    ("gemv_f16_4096x14336", "cold", "aware"): 118191293,
+    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1311128795,
+    ("hash_2p26_lf0.5_u64", "warm", "aware"): 20176573315,
+    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 544283743,
+    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 544654041,
+    ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245658056,
+    ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3932137976,
+    ("bfs_rmat22_ef16", "warm", "aware"): 239002624,
+    ("gemv_f32_4096x4096", "warm", "aware"): 67728661,
+    ("gemv_f32_4096x4096", "cold", "aware"): 67733792,
+    ("gemv_f16_14336x4096", "warm", "aware"): 117648532,
+    ("gemv_f16_14336x4096", "cold", "aware"): 117649803,
+    ("gemv_f16_4096x14336", "warm", "aware"): 117717623,
+    ("gemv_f16_4096x14336", "cold", "aware"): 117717546,
 }
 
 

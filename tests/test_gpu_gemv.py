@@ -262,3 +262,29 @@ def test_split_row_home_under_a_mask_without_the_die_bit(mode):
         assert int(torch.count_nonzero(ws[:8 * M])) == 0
     finally:
         assert _lib.lib.xd_set_home_mask(old) == 0
+
+
+def test_placements_on_queues_that_start_elsewhere():
+    """The three aware placements (split-row home route, whole-row home route, contiguous
+    eighths of the rows) on new streams, whose queues may deal workgroup 0 to another XCC,
+    before and after the library has learned the stream's offset: the oblivious kernel's bits."""
+    from l2domain_amd.domain import home_map
+    streams = [torch.cuda.Stream() for _ in range(4)]
+    for dtype, M, K in [("f32", 512, 4096), ("f16", 512, 4096), ("f16", 256, 14336)]:
+        if dtype == "f32":
+            A, x = gen.gemv_f32_inputs(M, K, seed=M + K)
+        else:
+            A, x = gen.gemv_f16_inputs(M, K, w_seed=M + K, x_seed=M + 2 * K)
+        base = run(A, x, "oblivious")
+        dA = device_aligned(A)
+        dx = torch.from_numpy(np.ascontiguousarray(x)).cuda()
+        home = home_map(dA)
+        ws = workspace(M, K, dA.dtype)
+        y = torch.empty(M, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        for s in streams:
+            for mode in ("aware", "rotated", "aware"):
+                gemv(dA, dx, y, mode=mode, home_attr=home, workspace=ws, stream=s)
+                s.synchronize()
+                np.testing.assert_array_equal(base.view(np.uint32), y.cpu().numpy().view(np.uint32))
+

@@ -151,3 +151,28 @@ def test_config_2p26_build_lookup(config_ref, mode):
     np.testing.assert_array_equal(host(v), rv)
     del t
     torch.cuda.empty_cache()
+
+
+def test_aware_on_queues_that_start_elsewhere():
+    """Range build and lookups in every mode on new streams, whose queues may deal workgroup 0
+    to another XCC, before and after the library has learned the stream's offset: found and
+    values bit-exact."""
+    slots, n = 1 << 20, 400000
+    keys, vals = ora.hash_kv(n + 50000, 21)
+    q = np.concatenate([keys[:n:3], keys[n:]])
+    ref = ora.HashTable(slots)
+    assert ref.build(keys[:n], vals[:n]) == 0
+    rv, rf = ref.lookup(q)
+    dk, dv, dq = dev(keys[:n]), dev(vals[:n]), dev(q)
+    torch.cuda.synchronize()
+    for s in [torch.cuda.Stream() for _ in range(4)]:
+        with torch.cuda.stream(s):
+            t = HashTable(slots)
+            for mode in ("aware", "rotated", "aware"):
+                t.build(dk, dv, mode=mode)
+                v, f = t.lookup(dq, mode=mode)
+                s.synchronize()
+                assert t.failures() == 0
+                np.testing.assert_array_equal(f.cpu().numpy(), rf)
+                np.testing.assert_array_equal(host(v), rv)
+

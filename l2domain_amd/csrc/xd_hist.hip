@@ -40,7 +40,7 @@ constexpr uint32_t kBucketBins = 1u << kHB;
 // routed tile. Longer tiles give the count pass longer runs (32768: count 176 us at 2^28
 // keys against 208 us at 16384); 24576 measured fastest for the XCD-aware call.
 constexpr int kTileKeys = 24576;
-static_assert(kTileKeys % 4096 == 0 && kTileKeys <= 65536, "tile shape");
+static_assert(kTileKeys % 4096 == 0 && kTileKeys < 65536, "tile shape (a tile's hot-key counts fit u16)");
 // u16 slots per tile in the workspace: 128 bytes past the tile, so that the runs of tiles 16
 // apart (those one count wave reads together) do not start at the same offset modulo 48 KiB.
 // At 2^28 Zipf keys the count pass took 86.5 us with tiles at kTileKeys, 79.8 / 80.3 / 81.1 us
@@ -119,11 +119,12 @@ static HistLayout hist_layout(size_t n, uint32_t num_bins) {
     o = align256(o + (size_t)L.ntiles * (L.nb + 1 + kPeelWords) * sizeof(uint32_t));
     L.part = o;
     o = align256(o + (size_t)L.ntiles * kPartStride * sizeof(uint16_t));
-    // hot-key table (kHotWords), then one row of kHotSlots counters per tile
+    // hot-key table (kHotWords), then one row of kHotSlots u16 counters per tile (a tile holds
+    // fewer than 2^16 keys)
     L.hot = o;
     o = align256(o + (size_t)kHotWords * sizeof(uint32_t));
     L.hot_part = o;
-    o = align256(o + (size_t)L.ntiles * kHotSlots * sizeof(uint32_t));
+    o = align256(o + (size_t)L.ntiles * kHotSlots * sizeof(uint16_t));
     // an 8 KiB chunk of all-ones keys (written by the sampling pass)
     L.ones = o;
     o = align256(o + kHomeChunk);
@@ -301,7 +302,7 @@ static_assert(kP1Threads / kWave * 4 * kP1Vec * (kWave * kPackBuckets / kColCoun
 template <int KIND, bool PACK>
 __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restrict__ part,
                                                uint32_t *__restrict__ offs, uint32_t *__restrict__ tot,
-                                               const uint32_t *__restrict__ hot, uint32_t *__restrict__ hot_part) {
+                                               const uint32_t *__restrict__ hot, uint16_t *__restrict__ hot_part) {
     // Every bucket's counter is split into S columns, column = lane % S (S = 64 for up to
     // 32 buckets), laid out col[b * S + s]: the lanes of one LDS add never share an address,
     // so a wave's 64 adds do not serialise on a popular bucket. col[kColCounters + s] and
@@ -534,7 +535,7 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
     // The range kind runs beside the lean kinds in calls with a hot-key table (the keys before
     // and after the vector tiles): its tiles add no hot counts, so their rows are zero, as the
     // count pass sums the rows of every tile. (The other generic kinds run without a table.)
-    if (KIND == kPartRange && hot != nullptr && tid < kHotSlots) hot_part[(size_t)t * kHotSlots + tid] = 0u;
+    if (KIND == kPartRange && hot != nullptr && tid < kHotSlots) hot_part[(size_t)t * kHotSlots + tid] = 0;
 
     const uint32_t nvec = (tile_total + 7) / 8;  // 8 u16 per 16-byte store
     const uint4 *from = reinterpret_cast<const uint4 *>(stage);
@@ -554,14 +555,14 @@ template <int KIND>
 __global__ void __launch_bounds__(kP1Threads) __attribute__((amdgpu_num_sgpr(kPartPackedSgprs)))
 hist_partition_packed_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restrict__ part,
                              uint32_t *__restrict__ offs, uint32_t *__restrict__ tot, const uint32_t *__restrict__ hot,
-                             uint32_t *__restrict__ hot_part) {
+                             uint16_t *__restrict__ hot_part) {
     partition_tile<KIND, true>(src, num_bins, nb, part, offs, tot, hot, hot_part);
 }
 
 template <int KIND>
 __global__ void __launch_bounds__(kP1Threads)
 hist_partition_kernel(PartSrc src, uint32_t num_bins, int nb, uint16_t *__restrict__ part, uint32_t *__restrict__ offs,
-                      uint32_t *__restrict__ tot, const uint32_t *__restrict__ hot, uint32_t *__restrict__ hot_part) {
+                      uint32_t *__restrict__ tot, const uint32_t *__restrict__ hot, uint16_t *__restrict__ hot_part) {
     partition_tile<KIND, false>(src, num_bins, nb, part, offs, tot, hot, hot_part);
 }
 
@@ -616,7 +617,7 @@ template <int KIND>
 __global__ void __launch_bounds__(kP1Threads) __attribute__((amdgpu_num_sgpr(kPartPackedSgprs)))
 hist_partition_lean_kernel(PartSrc src, uint32_t bound, int nb, uint16_t *__restrict__ part,
                            uint32_t *__restrict__ offs, uint32_t *__restrict__ tot, const uint32_t *__restrict__ hot,
-                           uint32_t *__restrict__ hot_part, const uint32_t *__restrict__ ones) {
+                           uint16_t *__restrict__ hot_part, const uint32_t *__restrict__ ones) {
     __shared__ __attribute__((aligned(16))) LeanLds S;
     const int g = (int)blockIdx.x;
     const int tid = (int)threadIdx.x;
@@ -806,7 +807,7 @@ hist_partition_lean_kernel(PartSrc src, uint32_t bound, int nb, uint16_t *__rest
         uint32_t c = 0;
 #pragma unroll
         for (int k = 0; k < kHotCopies; ++k) c += S.cnt[k * kLeanCopyStride + tid];
-        hot_part[(size_t)t * kHotSlots + my_perm] = c;
+        hot_part[(size_t)t * kHotSlots + my_perm] = (uint16_t)c;  // c <= kTileKeys < 2^16
     }
     const uint32_t nvec = (tile_total + 7) / 8;
     const uint4 *from = reinterpret_cast<const uint4 *>(S.stage);
@@ -907,11 +908,11 @@ __global__ void __launch_bounds__(kP2Threads)
 hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict__ offs, int nb, int ntiles,
                   const uint32_t *__restrict__ tot, int per_xcd, uint32_t *__restrict__ partials,
                   HistBucket *__restrict__ buckets, int mode, unsigned rot, uint32_t *__restrict__ hot_tab,
-                  const uint32_t *__restrict__ hot_part, XcdHint xh) {
+                  const uint16_t *__restrict__ hot_part, XcdHint xh) {
     __shared__ __attribute__((aligned(16))) uint32_t h[kCountSlots];
     __shared__ uint32_t wsum[kP2Waves];
     __shared__ int s_item[3];  // bucket (-1: idle slot), t0, t1
-    __shared__ uint32_t s_hot[kP2Threads];
+    __shared__ uint32_t s_hot[kP2Threads / (kHotSlots / 2) * kHotSlots];
     const int g = (int)blockIdx.x;
     const int tid = (int)threadIdx.x, lane = tid % kWave, wave = tid / kWave;
     int slot;
@@ -934,24 +935,31 @@ hist_count_kernel(const uint16_t *__restrict__ part, const uint32_t *__restrict_
     uint4 *h4 = reinterpret_cast<uint4 *>(h);
     for (int i = tid; i < (int)(kCountSlots / 4); i += kP2Threads) h4[i] = make_uint4(0, 0, 0, 0);
     // The hot-table counters: workgroup g sums the rows of tiles [g ntiles / G, (g + 1) ntiles
-    // / G) (G = the grid, whatever its bucket: four threads per row position, eight loads in
-    // flight each) and adds them to the positions' totals, which the merge adds to the keys'
-    // bins. (Summing each bucket's keys over its items' tile ranges read one or two lines
-    // of every row per item, and took 11.5 us of the 64 a median item ran at 2^28 Zipf keys.)
+    // / G) (G = the grid, whatever its bucket: each thread reads one 32-bit word, two row
+    // positions, of every 8th row, eight loads in flight) and adds them to the positions'
+    // totals, which the merge adds to the keys' bins. (Summing each bucket's keys over its
+    // items' tile ranges read one or two lines of every row per item, and took 11.5 us of the
+    // 64 a median item ran at 2^28 Zipf keys.)
     if (hot_tab != nullptr) {
         const int G = (int)gridDim.x;
         const int ta = (int)((long long)g * ntiles / G), tz = (int)((long long)(g + 1) * ntiles / G);
-        const int pos = tid % kHotSlots, q = tid / kHotSlots;
-        constexpr int Q = kP2Threads / kHotSlots, U = 8;
-        uint32_t acc = 0;
+        constexpr int W = kHotSlots / 2, Q = kP2Threads / W, U = 8;  // words per row, row streams
+        const int w = tid % W, q = tid / W;
+        const uint32_t *rows = reinterpret_cast<const uint32_t *>(hot_part);
+        uint32_t lo = 0, hi = 0;
         for (int tt = ta + q; tt < tz; tt += U * Q) {
             uint32_t v[U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) v[u] = hot_part[(size_t)min(tt + u * Q, tz - 1) * kHotSlots + pos];
+            for (int u = 0; u < U; ++u) v[u] = rows[(size_t)min(tt + u * Q, tz - 1) * W + w];
 #pragma unroll
-            for (int u = 0; u < U; ++u) acc += tt + u * Q < tz ? v[u] : 0u;
+            for (int u = 0; u < U; ++u) {
+                const uint32_t vv = tt + u * Q < tz ? v[u] : 0u;
+                lo += vv & 0xffffu;
+                hi += vv >> 16;
+            }
         }
-        s_hot[tid] = acc;
+        s_hot[q * kHotSlots + 2 * w] = lo;
+        s_hot[q * kHotSlots + 2 * w + 1] = hi;
         __syncthreads();
         if (tid < kHotSlots) {
             uint32_t sum = 0;
@@ -1252,16 +1260,16 @@ int xd_hist_u32(const uint32_t *keys, size_t n, uint32_t *counts, uint32_t num_b
     // Hot-key table: for calls of at least kHotMinKeys keys into at most kPackBuckets buckets
     // (the packed partition: the unpacked one has no registers left for the lookups).
     uint32_t *hot = nullptr;
-    uint32_t *hot_part = reinterpret_cast<uint32_t *>(ws + L.hot_part);
+    uint16_t *hot_part = reinterpret_cast<uint16_t *>(ws + L.hot_part);
     if (n >= kHotMinKeys && pack) {
         hot = reinterpret_cast<uint32_t *>(ws + L.hot);
         launch("hist_hot_kernel", hist_hot_kernel, dim3(1), dim3(1024), 0, s, keys, n, num_bins, L.nb, hot,
                reinterpret_cast<uint32_t *>(ws + L.ones));
         if (int rc = launch_status("hist_hot_kernel")) return rc;
     }
-    using PartKernel = void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *, const uint32_t *, uint32_t *);
+    using PartKernel = void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *, const uint32_t *, uint16_t *);
     using LeanKernel =
-        void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *, const uint32_t *, uint32_t *, const uint32_t *);
+        void (*)(PartSrc, uint32_t, int, uint16_t *, uint32_t *, uint32_t *, const uint32_t *, uint16_t *, const uint32_t *);
     for (int k = 0; k < nplan; ++k) {
         const PartLaunch &pl = plan[k];
         if (hot != nullptr && pl.kind != kPartRange) {

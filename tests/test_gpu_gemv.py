@@ -288,3 +288,31 @@ def test_placements_on_queues_that_start_elsewhere():
                 s.synchronize()
                 np.testing.assert_array_equal(base.view(np.uint32), y.cpu().numpy().view(np.uint32))
 
+
+def _random_shapes(n, seed):
+    """Seeded (dtype, M, K) draws over every route: K a multiple of 8 up to 16384 (fp16) or
+    4 up to 8192 (fp32), so rows of 1 to 4 whole chunks, rows inside a chunk and ragged rows."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        if rng.random() < 0.5:
+            out.append((np.float16, int(rng.integers(1, 3000)), 8 * int(rng.integers(1, 2049))))
+        else:
+            out.append((np.float32, int(rng.integers(1, 3000)), 4 * int(rng.integers(1, 2049))))
+    # the route boundaries themselves
+    out += [(np.float16, 1000, 4096), (np.float16, 999, 8192), (np.float32, 513, 2048), (np.float32, 77, 4096),
+            (np.float16, 5, 12288), (np.float32, 3, 10240)]
+    return out
+
+
+@pytest.mark.parametrize("dtype,M,K", _random_shapes(18, 2026))
+def test_random_shapes_integer_exact_all_modes(dtype, M, K):
+    """Integer inputs (exact in fp16 and fp32, |y| < 2^24) on seeded random shapes, 8 KiB-aligned
+    with a measured home map and a workspace: every mode equals the integer product."""
+    rng = np.random.default_rng(M * 7919 + K)
+    W = rng.integers(-8, 9, size=(M, K)).astype(dtype)
+    x = rng.integers(-3, 4, size=K).astype(dtype)
+    ref = (W.astype(np.int64) @ x.astype(np.int64)).astype(np.float32)
+    for mode in MODES:
+        np.testing.assert_array_equal(run(W, x, mode, mapped=True), ref, err_msg=f"{mode} {M}x{K}")
+

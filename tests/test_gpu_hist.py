@@ -198,3 +198,37 @@ def test_aware_on_queues_that_start_elsewhere():
             s.synchronize()
             np.testing.assert_array_equal(counts.cpu().numpy().view(np.uint32), ref)
 
+
+def _random_cases(n, seed):
+    """Seeded (n, num_bins, offset, skew) draws: sizes on both sides of the sampling threshold
+    (2^20 keys), bin counts from 1 to 2^24, keys starting 0 to 4095 words into their allocation
+    (routed head and tail pieces of every length), uniform or Zipf keys."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        out.append((int(rng.integers(1, 3 << 20)), int(2 ** rng.uniform(0, 24)), int(rng.integers(0, 4096)),
+                    bool(rng.random() < 0.5)))
+    return out
+
+
+@pytest.mark.parametrize("n,num_bins,offset,zipf", _random_cases(10, 2026))
+def test_random_sizes_offsets_all_modes(n, num_bins, offset, zipf):
+    """Every mode bit-exact against the oracle on seeded random shapes; some keys fall past
+    num_bins."""
+    rng = np.random.default_rng(n + num_bins + offset)
+    if zipf:
+        k = gen.zipf_keys_device(n + offset, min(num_bins, 1 << 20), 5000 + n, ZIPF_S).cpu().numpy().view(np.uint32).copy()
+    else:
+        k = rng.integers(0, num_bins + num_bins // 10 + 1, size=n + offset, dtype=np.int64).astype(np.uint32)
+    buf = torch.from_numpy(k.view(np.int32)).cuda()  # 256-byte aligned allocation
+    view = buf[offset:]
+    keys = k[offset:]
+    ref, _ = ora.histogram(keys, num_bins, nthreads=16)
+    h = Histogram(n, num_bins)
+    for mode in MODES:
+        counts = torch.full((num_bins,), -7, dtype=torch.int32, device="cuda")
+        h(view, counts, mode=mode)
+        torch.cuda.synchronize()
+        print(n, num_bins, offset, zipf, mode, flush=True)
+        np.testing.assert_array_equal(counts.cpu().numpy().view(np.uint32), ref)
+

@@ -176,3 +176,40 @@ def test_aware_on_queues_that_start_elsewhere():
                 np.testing.assert_array_equal(f.cpu().numpy(), rf)
                 np.testing.assert_array_equal(host(v), rv)
 
+
+def _random_tables(n, seed):
+    """Seeded (log2 slots, load factor, hit fraction, bulk build or inserts) draws."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(10, 23)), round(float(rng.uniform(0.05, 0.6)), 3), round(float(rng.uniform(0, 1)), 3),
+             bool(rng.random() < 0.5)) for _ in range(n)]
+
+
+@pytest.mark.parametrize("lg,lf,hits,bulk", _random_tables(10, 2026))
+def test_random_tables_all_modes(lg, lf, hits, bulk):
+    """Seeded random table sizes, load factors and hit fractions, built in bulk or by inserts and
+    looked up in every mode: found and values bit-exact against the oracle's serial table."""
+    slots = 1 << lg
+    n = max(1, int(slots * lf))
+    nq = max(1, n // 2)
+    keys, vals = ora.hash_kv(n + nq, lg * 1000 + n)
+    nh = int(nq * hits)
+    rng = np.random.default_rng(n)
+    q = np.concatenate([keys[rng.integers(0, n, size=nh)], keys[n:n + nq - nh]])
+    rng.shuffle(q)
+    ref = ora.HashTable(slots)
+    assert ref.build(keys[:n], vals[:n]) == 0
+    rv, rf = ref.lookup(q)
+    dk, dv, dq = dev(keys[:n]), dev(vals[:n]), dev(q)
+    for build_mode in MODES:
+        t = HashTable(slots)
+        if bulk:
+            t.build(dk, dv, mode=build_mode)
+        else:
+            t.insert(dk, dv, mode=build_mode)
+        for look_mode in MODES:
+            v, f = t.lookup(dq, mode=look_mode)
+            torch.cuda.synchronize()
+            assert t.failures() == 0
+            np.testing.assert_array_equal(f.cpu().numpy(), rf, err_msg=f"{build_mode} {look_mode}")
+            np.testing.assert_array_equal(host(v), rv, err_msg=f"{build_mode} {look_mode}")
+

@@ -167,3 +167,22 @@ def test_concurrent_host_threads():
         t.join(timeout=120)
     assert not any(t.is_alive() for t in threads)
     assert not errors, errors
+
+
+def _random_graphs(n, seed):
+    """Seeded (scale, edge factor, generator seed, source) draws of small R-MAT graphs."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(8, 17)), int(rng.integers(1, 33)), int(rng.integers(1, 1 << 30)),
+             int(rng.integers(0, 256))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("scale,ef,seed,src", _random_graphs(8, 2026))
+def test_random_rmat_all_modes(scale, ef, seed, src):
+    """Seeded random R-MAT graphs (sparse to dense, sources anywhere, isolated ones included):
+    levels bit-exact in every mode, from one route built per graph."""
+    rowptr, col = ora.rmat_csr(scale, ef, seed)
+    src = src % (len(rowptr) - 1)
+    g = Graph(rowptr, col)
+    for mode in MODES:
+        check(rowptr, col, src, mode, g)
+

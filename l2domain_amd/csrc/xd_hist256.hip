@@ -147,6 +147,22 @@ hist256_kernel(const uint32_t *__restrict__ words, uint64_t n, uint64_t pair0, u
         const uint32_t h0 = home.attr ? (uint32_t)lattr[a / kHomePage - home.page0] : home_of(a, home.mask & ~0x3fffull);
         return 2 * P + (h0 ^ want);
     };
+    // The wanted chunk of each of this workgroup's pairs, read from the staged map before the
+    // main loop: slot k's two bits (pair a, pair c) sit in lane k mod 64, bits 2 (k / 64) and
+    // 2 (k / 64) + 1, and the loop takes them with v_readlane. (Read from LDS inside the loop,
+    // each lookup waited for the slot's LDS adds issued before it: the LDS counter is in order.)
+    constexpr uint64_t kH8BitSlots = 16 * kWave;
+    const bool lanebits = routed && nslots <= kH8BitSlots;
+    uint32_t hb = 0;
+    if (lanebits) {
+        for (uint64_t k = lane, r = 0; k < nslots; k += kWave, ++r) {
+            const uint64_t Pa = pair0 + first + 2 * k * step;
+            const bool okc = 2 * k + 1 < npm;
+            const uint32_t ba = (uint32_t)(wanted(Pa) & 1u);
+            const uint32_t bc = (uint32_t)(wanted(okc ? Pa + step : Pa) & 1u);
+            hb |= (ba | (bc << 1)) << (2 * r);
+        }
+    }
     // slot k: vectors a and c, n = a valid | c valid << 1
     auto load_slot = [&](uint64_t k, uint4 &a, uint4 &c, uint32_t &nv) {
         uint64_t ca, cc;
@@ -155,6 +171,13 @@ hist256_kernel(const uint32_t *__restrict__ words, uint64_t n, uint64_t pair0, u
             const uint64_t P = pair0 + first + k * step;
             ca = 2 * P;
             cc = 2 * P + 1;
+        } else if (lanebits) {
+            const uint64_t Pa = pair0 + first + 2 * k * step;
+            okc = 2 * k + 1 < npm;
+            const uint32_t bits =
+                ((uint32_t)__builtin_amdgcn_readlane((int)hb, (int)(k & (kWave - 1))) >> (2 * (k / kWave))) & 3u;
+            ca = 2 * Pa + (bits & 1u);
+            cc = 2 * (okc ? Pa + step : Pa) + (bits >> 1);
         } else {
             const uint64_t Pa = pair0 + first + 2 * k * step;
             okc = 2 * k + 1 < npm;

@@ -51,8 +51,8 @@ TRAFFIC_SRC = "profiles/traffic_by_config.md (FETCH_SIZE/WRITE_SIZE runs of the 
 TRAFFIC = {
     ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1305536906,
     ("hash_2p26_lf0.5_u64", "warm", "aware"): 20176573315,
-    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 544283743,
-    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 544654041,
+    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 543642028,
+    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 543949562,
     ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245658056,
     ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3932137976,
     ("bfs_rmat22_ef16", "warm", "aware"): 239002624,

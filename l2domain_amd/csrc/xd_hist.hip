@@ -141,6 +141,16 @@ __device__ __forceinline__ uint4 load_stream(const uint4 *p) {
     return make_uint4(t.x, t.y, t.z, t.w);
 }
 
+// A 16-byte non-temporal store, for the partition's runs: 0.5 GiB at 2^28 keys, read once by
+// the count pass a pass later, never from cache. At 2^28 Zipf keys, aware: partition 208.3 ->
+// 207.1 us and count 68.6 -> 65.6 us against ordinary stores (the count pass no longer meets
+// the write-backs of the runs' dirty lines); contiguous tiles: 216.4 -> 220.1 and 70.1 ->
+// 64.9 us.
+__device__ __forceinline__ void store_stream(uint4 *p, const uint4 &v) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(v4u{v.x, v.y, v.z, v.w}, reinterpret_cast<v4u *>(p));
+}
+
 // ---------------------------------------------------------------------------------------
 // 0. hot keys (one workgroup): which keys the partition counts in LDS
 // ---------------------------------------------------------------------------------------
@@ -540,7 +550,7 @@ __device__ __forceinline__ void partition_tile(PartSrc src, uint32_t num_bins, i
     const uint32_t nvec = (tile_total + 7) / 8;  // 8 u16 per 16-byte store
     const uint4 *from = reinterpret_cast<const uint4 *>(stage);
     uint4 *dst = reinterpret_cast<uint4 *>(part + (size_t)t * kPartStride);
-    for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) dst[i] = from[i];
+    for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) store_stream(&dst[i], from[i]);
 }
 
 // Two workgroups of 16 waves share a CU only while a wave holds at most 80 scalar registers
@@ -812,7 +822,7 @@ hist_partition_lean_kernel(PartSrc src, uint32_t bound, int nb, uint16_t *__rest
     const uint32_t nvec = (tile_total + 7) / 8;
     const uint4 *from = reinterpret_cast<const uint4 *>(S.stage);
     uint4 *dst = reinterpret_cast<uint4 *>(part + (size_t)t * kPartStride);
-    for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) dst[i] = from[i];
+    for (uint32_t i = (uint32_t)tid; i < nvec; i += kP1Threads) store_stream(&dst[i], from[i]);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -49,7 +49,7 @@ MODES = ("oblivious", "aware", "rotated")
 # costs a request each way).
 TRAFFIC_SRC = "profiles/traffic_by_config.md (FETCH_SIZE/WRITE_SIZE runs of the commit named there)"
 TRAFFIC = {
-    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1305536906,
+    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1305539032,
     ("hash_2p26_lf0.5_u64", "warm", "aware"): 20176573315,
     ("hist256_bytes_512MiB_mix32", "warm", "aware"): 543642028,
     ("hist256_bytes_512MiB_mix32", "cold", "aware"): 543949562,

@@ -450,13 +450,25 @@ static int check_table(const void *table, uint64_t slots) {
 }
 
 // Grid for the probing kernels: a multiple of 8 so that every XCD gets the same number of
-// workgroups (workgroup i runs on XCD i mod 8); 16 workgroups per CU.
-static unsigned probe_grid(uint64_t n) {
+// workgroups (workgroup i runs on XCD i mod 8), at most `cap` workgroups (waves then walk
+// several 64-item chunks).
+constexpr uint64_t kWalkCap = 256 * 16;  // insert and routed probes: 16 workgroups per CU
+static unsigned probe_grid(uint64_t n, uint64_t cap = kWalkCap) {
     uint64_t g = (n + kHashThreads - 1) / kHashThreads;
-    const uint64_t cap = 256 * 16;
     if (g > cap) g = cap;
     g = (g + kNumXcd - 1) / kNumXcd * kNumXcd;
     return (unsigned)g;
+}
+
+// Lookups and dependent probes: oblivious calls give every wave one chunk and let the
+// dispatcher refill the CUs; the home modes, whose waves walk every chunk and keep about
+// half, cap the grid at 2^16 workgroups (each stages the table's page map in LDS). At 2^26
+// lookups into 2^27 slots, kernel µs oblivious / aware: 2202 / 2451 with 4096 workgroups,
+// 2207 / 2414 at 2^14, 2141 / 2285 at 2^16, 2090 / 2378 at one chunk per wave; the reference's dependent
+// probe (8 M queries) 552 / 407 against 535 / 396 at 2^16 or one chunk per wave.
+// (2^23 workgroups keep the dispatch's work-item count, a 32-bit field, at 2^31.)
+static unsigned lookup_grid(uint64_t n, int mode) {
+    return probe_grid(n, mode == XD_MODE_OBLIVIOUS ? (1ull << 23) : (1ull << 16));
 }
 
 }  // namespace xd
@@ -496,7 +508,7 @@ int xd_hash_lookup_u64(const void *table, uint64_t slots, const uint64_t *querie
     XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_hash_lookup_u64: bad mode");
     XD_REQUIRE(n < (1ull << 32), "xd_hash_lookup_u64: n must be < 2^32 per call");
     if (n == 0) return XD_OK;
-    launch("hash_lookup_kernel", hash_lookup_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+    launch("hash_lookup_kernel", hash_lookup_kernel, dim3(lookup_grid(n, mode)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<const Slot *>(table), slots - 1, queries, n, mode,
                        HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()}, vals_out,
                        found_out, xcd_hint((hipStream_t)stream));
@@ -512,7 +524,7 @@ int xd_dep_probe(const void *table, uint64_t slots, const int32_t *queries, uint
     XD_REQUIRE(chain_len >= 1 && chain_len <= 4096, "xd_dep_probe: chain_len must be in [1, 4096]");
     XD_REQUIRE(mode >= XD_MODE_OBLIVIOUS && mode <= XD_MODE_ROTATED, "xd_dep_probe: bad mode");
     if (n == 0) return XD_OK;
-    launch("dep_probe_kernel", dep_probe_kernel, dim3(probe_grid(n)), dim3(kHashThreads), 0, (hipStream_t)stream,
+    launch("dep_probe_kernel", dep_probe_kernel, dim3(lookup_grid(n, mode)), dim3(kHashThreads), 0, (hipStream_t)stream,
                        static_cast<const int2 *>(table), (uint32_t)(slots - 1), queries, n, chain_len, out, mode,
                        HomeMap{home_attr, reinterpret_cast<uint64_t>(table) / kHomePage, home_mask()},
                        xcd_hint((hipStream_t)stream));

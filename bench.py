@@ -49,19 +49,19 @@ MODES = ("oblivious", "aware", "rotated")
 # costs a request each way).
 TRAFFIC_SRC = "profiles/traffic_by_config.md (FETCH_SIZE/WRITE_SIZE runs of the commit named there)"
 TRAFFIC = {
-    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1305539032,
-    ("hash_2p26_lf0.5_u64", "warm", "aware"): 20176573315,
-    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 543642028,
-    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 543949562,
-    ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245658056,
-    ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3932137976,
-    ("bfs_rmat22_ef16", "warm", "aware"): 239002624,
-    ("gemv_f32_4096x4096", "warm", "aware"): 67728661,
-    ("gemv_f32_4096x4096", "cold", "aware"): 67733792,
-    ("gemv_f16_14336x4096", "warm", "aware"): 117648532,
-    ("gemv_f16_14336x4096", "cold", "aware"): 117649803,
-    ("gemv_f16_4096x14336", "warm", "aware"): 117717623,
-    ("gemv_f16_4096x14336", "cold", "aware"): 117717546,
+    ("hist_2p28_zipf1.1_2p20bins", "warm", "aware"): 1305528162,
+    ("hash_2p26_lf0.5_u64", "warm", "aware"): 19910025236,
+    ("hist256_bytes_512MiB_mix32", "warm", "aware"): 543800710,
+    ("hist256_bytes_512MiB_mix32", "cold", "aware"): 544154466,
+    ("bfs_ref_V2M_deg64_src4096_depth4", "warm", "aware"): 245717927,
+    ("hash_dep_K32M_Q8M_C2p26_L4", "warm", "aware"): 3927067605,
+    ("bfs_rmat22_ef16", "warm", "aware"): 239020958,
+    ("gemv_f32_4096x4096", "warm", "aware"): 67730532,
+    ("gemv_f32_4096x4096", "cold", "aware"): 67736254,
+    ("gemv_f16_14336x4096", "warm", "aware"): 117648613,
+    ("gemv_f16_14336x4096", "cold", "aware"): 117649957,
+    ("gemv_f16_4096x14336", "warm", "aware"): 117821674,
+    ("gemv_f16_4096x14336", "cold", "aware"): 117821669,
 }
 
 

@@ -266,9 +266,12 @@ size_t xd_gemv_workspace_size(int M, int K, int elem_bytes);
  *                      xd_gemv_workspace_size() bytes, 8-byte aligned, zero-filled once when
  *                      allocated; each call leaves it zeroed; calls sharing one workspace
  *                      must not overlap).
- *                      Otherwise every XCD gets one contiguous eighth of the rows (the
- *                      reference's per-side row lists, GEMV.cu:264-273);
- *   XD_MODE_ROTATED    the same routes with the far die / next XCD (the "swapped" control).
+ *                      Otherwise (rows that straddle 8 KiB chunks, no workspace, A not
+ *                      8 KiB aligned) no die placement applies and the rows keep the
+ *                      oblivious order, which measured faster than one contiguous eighth
+ *                      of the rows per XCD;
+ *   XD_MODE_ROTATED    the home routes with the far die; otherwise each XCD takes a
+ *                      rotated contiguous eighth of the rows (the "swapped" control).
  * The split-row route gives bit-identical y to XD_MODE_OBLIVIOUS for S = 2 and 4. */
 int xd_gemv_f32(const float *A, const float *x, float *y, int M, int K, int mode, const uint8_t *home_attr,
                 void *workspace, size_t workspace_bytes, void *stream);

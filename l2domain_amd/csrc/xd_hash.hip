@@ -464,9 +464,9 @@ static unsigned probe_grid(uint64_t n, uint64_t cap = kWalkCap) {
 // dispatcher refill the CUs; the home modes, whose waves walk every chunk and keep about
 // half, cap the grid at 2^16 workgroups (each stages the table's page map in LDS). At 2^26
 // lookups into 2^27 slots, kernel µs oblivious / aware: 2202 / 2451 with 4096 workgroups,
-// 2207 / 2414 at 2^14, 2141 / 2285 at 2^16, 2090 / 2378 at one chunk per wave (aware 2315 at 2^15,
-// 2310 at 2^17); the reference's dependent
-// probe (8 M queries) 552 / 407 against 535 / 396 at 2^16 or one chunk per wave.
+// 2207 / 2414 at 2^14, 2141 / 2285 at 2^16, 2090 / 2378 at one chunk per wave (aware 2315 at
+// 2^15 and 2310 at 2^17); the reference's dependent probe (8 M queries) 552 / 407 against
+// 535 / 396 at 2^16 or one chunk per wave.
 // (2^23 workgroups keep the dispatch's work-item count, a 32-bit field, at 2^31.)
 static unsigned lookup_grid(uint64_t n, int mode) {
     return probe_grid(n, mode == XD_MODE_OBLIVIOUS ? (1ull << 23) : (1ull << 16));

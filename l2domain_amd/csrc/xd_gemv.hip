@@ -95,7 +95,8 @@ gemv_kernel(const uint4 *__restrict__ A, const uint4 *__restrict__ x, float *__r
 // Exact-width variant: each row is split into S segments of 64*CW vectors, one wave per
 // segment, so every lane owns exactly CW vectors and no load needs a bounds check. The
 // first row's loads are issued before the lane's CW x vectors, which stay in registers for
-// every row; with DB the wave's next row is loaded while the current one is reduced.
+// every row; with DB the wave's next row is loaded while the current one is reduced (the
+// launcher gives every workgroup one pass of rows, so no wave has a next row there).
 // Partial sums of a split row meet in LDS.
 template <bool F16, int CW, int S, bool DB>
 __global__ void __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4)))
@@ -377,7 +378,8 @@ static int seg_per_row(int K, int elem_bytes) {
 }
 
 static int rows_per_workgroup(int M, int nv) {
-    // Aim for >= 4 workgroups per CU on 256 CUs and one row per wave for long rows.
+    // (the generic kernel, rows of a length that is not a multiple of 64 vectors) Aim for
+    // >= 4 workgroups per CU on 256 CUs and one row per wave for long rows.
     int rpw = kGemvWaves;
     while ((long long)M / (rpw * 2) >= 1024 && nv * 16 * rpw * 2 <= 256 * 1024) rpw *= 2;
     return rpw;
